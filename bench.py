@@ -1,0 +1,208 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path: forward + backward of causal_conv1d_fn on one MI355X.
+
+Workload (BASELINE.json metric): x (4, 8192, 1024) bf16 ~N(0,1), weight (1024, 4) fp32 ~N(0, 1/4),
+bias (1024) fp32 ~N(0,1), activation silu, upstream gradient (4, 8192, 1024) bf16 ~N(0,1). One step =
+out = causal_conv1d_fn(x, w, b, activation="silu") followed by the gradients of x, w and b
+(torch.autograd.grad, so nothing is accumulated). Input sets rotate (4 sets of x and dy, 512 MiB, twice
+the 256 MiB Infinity Cache) so every step reads its inputs from HBM. Steps are captured once per input
+set in a HIP graph and replayed, which removes Python launch overhead from the device timeline; the
+eager (un-captured) rate is reported beside it.
+
+Prints one JSON line. `value` is the step's algorithmic HBM bytes (read x, write out; read x, read dy,
+write dx; plus weights and bias) divided by the measured step time, in GB/s.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+_ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(_ROOT, "causal-conv1d-triton_amd"))
+
+METRIC = "fwd+bwd latency (us) and achieved HBM GB/s vs peak, bf16 B=4 T=8192 D=1024 W=4"
+PEAK_GBS = 8000.0  # MI355X HBM3E, public spec
+
+
+def alg_bytes(B, T, D, W, ex=2, ew=4, eb=4):
+    """Algorithmic HBM bytes of one forward and one backward pass (weights and bias read once per
+    pass; the backward also writes dweight and dbias). The backward's fp32 partial-sum workspace is
+    excluded: it is implementation traffic, reported by the rocprof counters."""
+    n = B * T * D
+    fwd = n * (ex + ex) + D * W * ew + D * eb
+    bwd = n * (ex + ex + ex) + 2 * D * W * ew + 2 * D * eb
+    return fwd, bwd
+
+
+def _capture(fn, warm_stream):
+    """Warms fn up on a side stream (as torch requires before capture) and captures it."""
+    warm_stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(warm_stream):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(warm_stream)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def _time_graphs(graphs, steps, warmup):
+    for k in range(warmup):
+        graphs[k % len(graphs)].replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for k in range(steps):
+        graphs[k % len(graphs)].replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_baseline(seconds):
+    """The CPU oracle (a single-threaded C restatement of the reference algorithm) on a bounded
+    sample of the workload: one of the four batch rows, forward + backward, repeated for about
+    `seconds` seconds. Reported in the metric's unit (algorithmic GB/s)."""
+    sys.path.insert(0, os.path.join(_ROOT, "oracle"))
+    import numpy as np
+
+    import ccv1d_oracle
+
+    B, T, D, W = 1, 8192, 1024, 4
+    g = np.random.default_rng(0)
+    x = g.standard_normal((B, T, D), dtype=np.float32)
+    w = (g.standard_normal((D, W), dtype=np.float32) / 2).astype(np.float32)
+    b = g.standard_normal(D, dtype=np.float32)
+    dy = g.standard_normal((B, T, D), dtype=np.float32)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        ccv1d_oracle.fwd(x, w, b, silu=True)
+        ccv1d_oracle.bwd(x, w, dy, b, silu=True)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 1000:
+            break
+    fwd_b, bwd_b = alg_bytes(B, T, D, W)
+    return {
+        "value": round((fwd_b + bwd_b) * reps / el / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"oracle/ccv1d_oracle.c fwd+bwd, B=1 T=8192 D=1024 W=4 bias+silu (1/4 of the "
+                  f"workload), {reps} reps in {el:.1f} s; ms_per_step_equiv="
+                  f"{el / reps * 4 * 1e3:.1f}",
+        "host_cpus": os.cpu_count(),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sets", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-eager", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU; the op needs no collective (see DESIGN.md, "
+              "sharding). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from causal_conv1d_triton import causal_conv1d_fn
+    from causal_conv1d_triton.causal_conv1d import _bwd, _fwd
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, T, D, W = 4, 8192, 1024, 4
+    gen = torch.Generator(device=dev).manual_seed(0)
+    w = (torch.randn(D, W, generator=gen, device=dev) / 2).requires_grad_(True)
+    b = torch.randn(D, generator=gen, device=dev).requires_grad_(True)
+    sets = []
+    for _ in range(args.sets):
+        x = torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16).requires_grad_(True)
+        dy = torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
+        sets.append((x, dy))
+    torch.cuda.synchronize()
+
+    def step(i):
+        x, dy = sets[i]
+        out = causal_conv1d_fn(x, w, b, activation="silu")
+        return torch.autograd.grad(out, (x, w, b), dy)
+
+    side = torch.cuda.Stream()
+    results = []
+    step_graphs = [_capture(lambda i=i: results.append(step(i)), side) for i in range(args.sets)]
+    results.clear()
+    ms_step = _time_graphs(step_graphs, args.steps, args.warmup)
+
+    # Per-pass device time of the two launches that make up a step, each captured on its own.
+    fwd_graphs = [_capture(lambda i=i: _fwd(sets[i][0].detach(), w.detach(), b.detach(), None,
+                                            None, None, True), side) for i in range(args.sets)]
+    bwd_graphs = [_capture(lambda i=i: _bwd(sets[i][0].detach(), w.detach(), b.detach(), None,
+                                            None, sets[i][1], None, False, True), side)
+                  for i in range(args.sets)]
+    ms_fwd = _time_graphs(fwd_graphs, args.steps, args.warmup)
+    ms_bwd = _time_graphs(bwd_graphs, args.steps, args.warmup)
+
+    eager_ms = None
+    if not args.no_eager:
+        for k in range(args.warmup):
+            step(k % args.sets)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(args.steps):
+            step(k % args.sets)
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    fwd_b, bwd_b = alg_bytes(B, T, D, W)
+    gbs = (fwd_b + bwd_b) / (ms_step * 1e-3) / 1e9
+    bwd_gbs = bwd_b / (ms_bwd * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "latency_us": round(ms_step * 1e3, 2),
+        "frac_of_peak": round(gbs / PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "causal_conv1d_fn fwd+bwd, bias+silu (BASELINE configs[1] at T=8192)",
+            "batch": B, "seqlen": T, "dim": D, "width": W,
+            "x_dtype": "bf16", "weight_dtype": "fp32", "input_sets": args.sets,
+            "timing": "hip graph replay per input set, events around the timed steps",
+        },
+        "passes_us": {"fwd": round(ms_fwd * 1e3, 2), "bwd": round(ms_bwd * 1e3, 2)},
+        "eager_ms_per_step": None if eager_ms is None else round(eager_ms, 4),
+        "roofline": {
+            "kernel": "backward pass (bwd_fast_kernel + reduce_partials_kernel)",
+            "bound": "hbm",
+            "achieved": round(bwd_gbs, 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(bwd_gbs / PEAK_GBS, 4),
+            "traffic": None,
+            "alg_bytes": bwd_b,
+        },
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

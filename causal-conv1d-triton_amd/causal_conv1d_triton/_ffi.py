@@ -1,0 +1,143 @@
+"""ctypes binding of libccv1d.so, the C ABI declared in include/ccv1d.h.
+
+The library is the only compute path: if it is missing or fails to load, every call raises. It must be
+loaded after `import torch` so that it binds to the HIP runtime torch has already loaded (same
+soname), which makes torch's streams and device pointers valid arguments.
+"""
+
+import ctypes
+import os
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libccv1d.so")
+
+DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_ptr = ctypes.c_void_p
+
+_lib = None
+
+
+class CCV1DError(RuntimeError):
+    """A libccv1d call returned an error status."""
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Loads libccv1d.so once and declares the signatures of its exports."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        raise RuntimeError(
+            f"{_LIB_PATH} is not built; run `make -C causal-conv1d-triton_amd` "
+            "(or __graft_entry__.build()) first"
+        )
+    lib = ctypes.CDLL(_LIB_PATH)
+    lib.ccv1d_abi_version.restype = _c_int
+    lib.ccv1d_abi_version.argtypes = []
+    lib.ccv1d_last_error.restype = ctypes.c_char_p
+    lib.ccv1d_last_error.argtypes = []
+    lib.ccv1d_fwd.restype = _c_int
+    lib.ccv1d_fwd.argtypes = [
+        _c_ptr, _c_i64, _c_i64, _c_int,  # x, strides, dtype
+        _c_ptr, _c_int,  # weight
+        _c_ptr, _c_int,  # bias
+        _c_ptr,  # seq_idx
+        _c_ptr, _c_int,  # initial_states
+        _c_ptr, _c_ptr,  # out, final_states
+        _c_i64, _c_i64, _c_i64, _c_i64,  # batch, seqlen, dim, width
+        _c_int, _c_int, _c_ptr,  # silu, device, stream
+    ]
+    lib.ccv1d_bwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.ccv1d_bwd_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]
+    lib.ccv1d_bwd.restype = _c_int
+    lib.ccv1d_bwd.argtypes = [
+        _c_ptr, _c_i64, _c_i64, _c_int,  # x
+        _c_ptr, _c_int,  # weight
+        _c_ptr, _c_int,  # bias
+        _c_ptr,  # seq_idx
+        _c_ptr, _c_int,  # initial_states
+        _c_ptr, _c_i64, _c_i64,  # dout, strides
+        _c_ptr,  # dfinal_states
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # dx, dinitial_states, dweight, dbias
+        _c_ptr, ctypes.c_size_t,  # workspace, bytes
+        _c_i64, _c_i64, _c_i64, _c_i64,  # batch, seqlen, dim, width
+        _c_int, _c_int, _c_ptr,  # silu, device, stream
+    ]
+    _lib = lib
+    return lib
+
+
+def _code(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _check(rc: int, lib) -> None:
+    if rc != 0:
+        raise CCV1DError(f"libccv1d error {rc}: {lib.ccv1d_last_error().decode()}")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def fwd(x, weight, bias, seq_idx, initial_states, out, final_states, silu: bool) -> None:
+    lib = load()
+    B, T, D = x.shape
+    W = weight.shape[1]
+    dev = x.device
+    rc = lib.ccv1d_fwd(
+        x.data_ptr(), x.stride(0), x.stride(1), _code(x),
+        weight.data_ptr(), _code(weight),
+        _ptr(bias), 0 if bias is None else _code(bias),
+        _ptr(seq_idx),
+        _ptr(initial_states), 0 if initial_states is None else _code(initial_states),
+        out.data_ptr(), _ptr(final_states),
+        B, T, D, W,
+        int(silu), dev.index, _stream(dev),
+    )
+    _check(rc, lib)
+
+
+def bwd_workspace_bytes(B: int, T: int, D: int, W: int, x_dtype: torch.dtype) -> int:
+    return load().ccv1d_bwd_workspace_bytes(B, T, D, W, DTYPE_CODES.get(x_dtype, 0))
+
+
+def bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit, dweight, dbias,
+        workspace, silu: bool) -> None:
+    lib = load()
+    B, T, D = x.shape
+    W = weight.shape[1]
+    dev = x.device
+    if dout.dtype != x.dtype:
+        raise TypeError(f"dout dtype {dout.dtype} differs from x dtype {x.dtype}")
+    if dfinal_states is not None and dfinal_states.dtype != x.dtype:
+        raise TypeError(f"dfinal_states dtype {dfinal_states.dtype} differs from x dtype {x.dtype}")
+    rc = lib.ccv1d_bwd(
+        x.data_ptr(), x.stride(0), x.stride(1), _code(x),
+        weight.data_ptr(), _code(weight),
+        _ptr(bias), 0 if bias is None else _code(bias),
+        _ptr(seq_idx),
+        _ptr(initial_states), 0 if initial_states is None else _code(initial_states),
+        dout.data_ptr(), dout.stride(0), dout.stride(1),
+        _ptr(dfinal_states),
+        dx.data_ptr(), _ptr(dinit), dweight.data_ptr(), _ptr(dbias),
+        _ptr(workspace), 0 if workspace is None else workspace.numel(),
+        B, T, D, W,
+        int(silu), dev.index, _stream(dev),
+    )
+    _check(rc, lib)

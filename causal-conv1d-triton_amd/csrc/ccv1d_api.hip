@@ -1,0 +1,366 @@
+// C ABI of libccv1d.so (declared in include/ccv1d.h): argument validation, the empty-input paths,
+// the choice between the vectorised and the generic kernels, time tiling, and launches on the
+// caller's stream. This is the host launcher layer of the reference (`_fwd`, `_bwd`, `_chunking`;
+// causal_conv1d.py:377-541) moved into native code.
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+
+#include "ccv1d.h"
+#include "ccv1d_launch.h"
+
+using namespace ccv1d;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(CCV1D_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool valid_dt(int dt) { return dt >= CCV1D_F32 && dt <= CCV1D_F64; }
+
+int vec_of(int x_dt) { return x_dt == CCV1D_F32 ? 4 : 8; }  // 16-byte vectors
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Row tiling overrides for tuning sweeps, read once: CCV1D_FWD_ROWS / CCV1D_BWD_ROWS (rows per tile
+// of the vectorised kernels; a power of two in [8, 1024]).
+struct Tune {
+  int fwd_rows = 0;
+  int bwd_rows = 0;
+};
+
+const Tune& tune() {
+  static const Tune t = [] {
+    Tune v;
+    auto rd = [](const char* name) {
+      const char* e = std::getenv(name);
+      if (!e) return 0;
+      const int r = std::atoi(e);
+      return (r >= 8 && r <= 1024 && (r & (r - 1)) == 0) ? r : 0;
+    };
+    v.fwd_rows = rd("CCV1D_FWD_ROWS");
+    v.bwd_rows = rd("CCV1D_BWD_ROWS");
+    return v;
+  }();
+  return t;
+}
+
+// Tiling of the vectorised kernels: the longest tile (fewest halo re-reads) that still gives the
+// grid `target_waves` waves, a function of the shape alone so that results, including the dweight
+// summation order, do not depend on the device.
+Tiling fast_tiling(int64_t B, int64_t T, int64_t D, int vec, int nw, int lmin, int lmax,
+                   int64_t target_waves, int override_rows) {
+  Tiling t{};
+  const int64_t G = D / vec;
+  t.nGW = (int32_t)cdiv(G, 64);
+  int L = lmax;
+  if (override_rows > 0) {
+    L = override_rows;
+  } else {
+    while (L > lmin && B * cdiv(T, L) * t.nGW < target_waves) L >>= 1;
+  }
+  t.L = L;
+  t.nT = (int32_t)cdiv(T, L);
+  t.nTB = (int32_t)cdiv(t.nT, nw);
+  t.nBlk = (int32_t)(B * t.nGW * t.nTB);
+  return t;
+}
+
+Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
+  return fast_tiling(B, T, D, vec_of(x_dt), kFwdNW, 16, 64, 4096, tune().fwd_rows);
+}
+
+Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
+  return fast_tiling(B, T, D, vec_of(x_dt), kBwdNW, 32, 64, 2048, tune().bwd_rows);
+}
+
+Tiling generic_tiling(int64_t T) {
+  Tiling t{};
+  t.L = kGenericL;
+  t.nT = (int32_t)cdiv(T, kGenericL);
+  return t;
+}
+
+// Restores the calling thread's current device on scope exit.
+struct DeviceGuard {
+  int prev = -1;
+  bool changed = false;
+  hipError_t err = hipSuccess;
+  explicit DeviceGuard(int dev) {
+    err = hipGetDevice(&prev);
+    if (err == hipSuccess && prev != dev) {
+      err = hipSetDevice(dev);
+      changed = err == hipSuccess;
+    }
+  }
+  ~DeviceGuard() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+int check_common(const void* x, int64_t s_xb, int64_t s_xt, int x_dt, const void* w, int w_dt,
+                 const void* bias, int b_dt, const void* init, int i_dt, int64_t B, int64_t T,
+                 int64_t D, int64_t W) {
+  if (B < 0 || T < 0 || D < 0) return fail(CCV1D_ERR_INVALID, "negative shape (%lld, %lld, %lld)",
+                                           (long long)B, (long long)T, (long long)D);
+  if (W < 2) return fail(CCV1D_ERR_INVALID, "width must be >= 2 (got %lld)", (long long)W);
+  if (!valid_dt(x_dt) || !valid_dt(w_dt) || (bias && !valid_dt(b_dt)) || (init && !valid_dt(i_dt)))
+    return fail(CCV1D_ERR_INVALID, "bad dtype code");
+  if (s_xb < 0 || s_xt < 0) return fail(CCV1D_ERR_INVALID, "negative stride");
+  if (D > 0 && !w) return fail(CCV1D_ERR_INVALID, "weight is null");
+  if (B * T * D > 0 && !x) return fail(CCV1D_ERR_INVALID, "x is null");
+  if (D > 0 && (T + W) * (s_xt > D ? s_xt : D) >= (int64_t(1) << 31))
+    return fail(CCV1D_ERR_INVALID, "(seqlen + width) * max(x time stride, dim) must be < 2^31");
+  if (B >= (int64_t(1) << 31) || D >= (int64_t(1) << 31))
+    return fail(CCV1D_ERR_INVALID, "batch and dim must be < 2^31");
+  return CCV1D_OK;
+}
+
+// The vectorised kernels need 16-byte rows: dim a multiple of the vector, aligned bases and strides.
+bool fast_ok(int x_dt, int64_t D, int64_t W, const void* x, int64_t s_xb, int64_t s_xt) {
+  if (W > kMaxFastW || x_dt == CCV1D_F64) return false;
+  const int v = vec_of(x_dt);
+  return D % v == 0 && aligned16(x) && s_xb % v == 0 && s_xt % v == 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ccv1d_abi_version(void) { return CCV1D_ABI_VERSION; }
+
+const char* ccv1d_last_error(void) { return g_last_error.c_str(); }
+
+int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+              const void* weight, int weight_dtype, const void* bias, int bias_dtype,
+              const int32_t* seq_idx, const void* initial_states, int init_dtype, void* out,
+              void* final_states, int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+              int silu, int device, void* stream) {
+  g_last_error.clear();
+  const int64_t B = batch, T = seqlen, D = dim, W = width, P = W - 1;
+  int rc = check_common(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
+                        initial_states, init_dtype, B, T, D, W);
+  if (rc) return rc;
+  if (seq_idx && final_states)
+    return fail(CCV1D_ERR_INVALID, "cannot return final states if seq_idx is given");
+  if (B * T * D > 0 && !out) return fail(CCV1D_ERR_INVALID, "out is null");
+  if (B * D == 0) return CCV1D_OK;
+  const bool fast = T > 0 && fast_ok(x_dtype, D, W, x, x_stride_b, x_stride_t) && aligned16(out) &&
+                    (!final_states || aligned16(final_states));
+  Tiling tl{};
+  if (T > 0) {
+    if (fast) {
+      tl = fwd_fast_tiling(B, T, D, x_dtype);
+    } else {
+      if (W > kMaxGenericW) return fail(CCV1D_ERR_UNSUPPORTED, "width > %d", kMaxGenericW);
+      tl = generic_tiling(T);
+      if (B * tl.nT >= (int64_t(1) << 31) || cdiv(D, 64) > 65535)
+        return fail(CCV1D_ERR_UNSUPPORTED, "shape too large for the generic kernel");
+    }
+  }
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (T == 0) {
+    // With no rows, the final states are the initial states (causal_conv1d.py:437-444).
+    if (final_states) {
+      const hipError_t e = launch_fill(final_states, x_dtype, initial_states, init_dtype, B * P * D, s);
+      if (e != hipSuccess) return hip_fail(e, "fill launch");
+    }
+    return CCV1D_OK;
+  }
+
+  FwdParams p{};
+  p.x = x;
+  p.w = weight;
+  p.bias = bias;
+  p.seq = seq_idx;
+  p.init = initial_states;
+  p.out = out;
+  p.fin = final_states;
+  p.s_xb = x_stride_b;
+  p.s_xt = (int32_t)x_stride_t;
+  p.B = (int32_t)B;
+  p.T = (int32_t)T;
+  p.D = (int32_t)D;
+  p.W = (int32_t)W;
+  p.w_dt = weight_dtype;
+  p.b_dt = bias_dtype;
+  p.i_dt = init_dtype;
+  p.has_bias = bias != nullptr;
+  p.has_init = initial_states != nullptr;
+  p.has_final = final_states != nullptr;
+  p.silu = silu != 0;
+
+  p.tl = tl;
+  hipError_t e;
+  if (fast) {
+    switch (x_dtype) {
+      case CCV1D_BF16: e = launch_fwd_fast_t<__bf16>(p, s); break;
+      case CCV1D_F16: e = launch_fwd_fast_t<_Float16>(p, s); break;
+      default: e = launch_fwd_fast_t<float>(p, s); break;
+    }
+  } else {
+    switch (x_dtype) {
+      case CCV1D_BF16: e = launch_fwd_generic_t<__bf16>(p, s); break;
+      case CCV1D_F16: e = launch_fwd_generic_t<_Float16>(p, s); break;
+      case CCV1D_F32: e = launch_fwd_generic_t<float>(p, s); break;
+      default: e = launch_fwd_generic_t<double>(p, s); break;
+    }
+  }
+  if (e != hipSuccess) return hip_fail(e, "forward launch");
+  return CCV1D_OK;
+}
+
+size_t ccv1d_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+                                 int x_dtype) {
+  const int64_t B = batch, T = seqlen, D = dim, W = width;
+  if (B <= 0 || T <= 0 || D <= 0 || W < 2 || !valid_dt(x_dtype)) return 0;
+  int64_t rows = B * generic_tiling(T).nT;
+  if (W <= kMaxFastW && x_dtype != CCV1D_F64) {
+    const int64_t fr = B * bwd_fast_tiling(B, T, D, x_dtype).nTB;
+    if (fr > rows) rows = fr;
+  }
+  return (size_t)(rows * (W + 1) * D * (int64_t)sizeof(float));
+}
+
+int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+              const void* weight, int weight_dtype, const void* bias, int bias_dtype,
+              const int32_t* seq_idx, const void* initial_states, int init_dtype,
+              const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
+              const void* dfinal_states, void* dx, void* dinitial_states, void* dweight,
+              void* dbias, void* workspace, size_t workspace_bytes, int64_t batch, int64_t seqlen,
+              int64_t dim, int64_t width, int silu, int device, void* stream) {
+  g_last_error.clear();
+  const int64_t B = batch, T = seqlen, D = dim, W = width, P = W - 1;
+  int rc = check_common(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
+                        initial_states, init_dtype, B, T, D, W);
+  if (rc) return rc;
+  if (dout_stride_b < 0 || dout_stride_t < 0) return fail(CCV1D_ERR_INVALID, "negative stride");
+  if (D > 0 && (T + W) * (dout_stride_t > D ? dout_stride_t : D) >= (int64_t(1) << 31))
+    return fail(CCV1D_ERR_INVALID, "(seqlen + width) * max(dout time stride, dim) must be < 2^31");
+  if (B * T * D > 0 && (!dout || !dx)) return fail(CCV1D_ERR_INVALID, "dout or dx is null");
+  if (D > 0 && !dweight) return fail(CCV1D_ERR_INVALID, "dweight is null");
+  if ((bias != nullptr) != (dbias != nullptr))
+    return fail(CCV1D_ERR_INVALID, "dbias must be given exactly when bias is");
+  if (dinitial_states && !initial_states)
+    return fail(CCV1D_ERR_INVALID, "dinitial_states requires initial_states");
+  if (seq_idx && dfinal_states)
+    return fail(CCV1D_ERR_INVALID, "cannot take final-state gradients if seq_idx is given");
+  if (D == 0) return CCV1D_OK;
+  const bool empty = B == 0 || T == 0;
+  const bool fast = !empty && fast_ok(x_dtype, D, W, x, x_stride_b, x_stride_t) &&
+                    fast_ok(x_dtype, D, W, dout, dout_stride_b, dout_stride_t) && aligned16(dx) &&
+                    (!dfinal_states || aligned16(dfinal_states)) && aligned16(workspace);
+  Tiling tl{};
+  int64_t rows = 0;
+  if (!empty) {
+    if (fast) {
+      tl = bwd_fast_tiling(B, T, D, x_dtype);
+      rows = B * tl.nTB;
+    } else {
+      if (W > kMaxGenericW) return fail(CCV1D_ERR_UNSUPPORTED, "width > %d", kMaxGenericW);
+      tl = generic_tiling(T);
+      rows = B * tl.nT;
+      if (rows >= (int64_t(1) << 31) || cdiv(D, 64) > 65535)
+        return fail(CCV1D_ERR_UNSUPPORTED, "shape too large for the generic kernel");
+    }
+    const size_t need = (size_t)(rows * (W + 1) * D * (int64_t)sizeof(float));
+    if (!workspace || workspace_bytes < need)
+      return fail(CCV1D_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes,
+                  need);
+  }
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (empty) {
+    // No outputs: dweight = dbias = 0, and the initial-state gradient is the final-state gradient
+    // (causal_conv1d.py:480-489).
+    hipError_t e = launch_fill(dweight, weight_dtype, nullptr, 0, D * W, s);
+    if (e == hipSuccess && dbias) e = launch_fill(dbias, bias_dtype, nullptr, 0, D, s);
+    if (e == hipSuccess && dinitial_states)
+      e = launch_fill(dinitial_states, init_dtype, dfinal_states, x_dtype, B * P * D, s);
+    if (e != hipSuccess) return hip_fail(e, "fill launch");
+    return CCV1D_OK;
+  }
+
+  BwdParams p{};
+  p.x = x;
+  p.w = weight;
+  p.bias = bias;
+  p.seq = seq_idx;
+  p.init = initial_states;
+  p.dy = dout;
+  p.dfin = dfinal_states;
+  p.dx = dx;
+  p.dinit = dinitial_states;
+  p.part = static_cast<float*>(workspace);
+  p.s_xb = x_stride_b;
+  p.s_yb = dout_stride_b;
+  p.s_xt = (int32_t)x_stride_t;
+  p.s_yt = (int32_t)dout_stride_t;
+  p.B = (int32_t)B;
+  p.T = (int32_t)T;
+  p.D = (int32_t)D;
+  p.W = (int32_t)W;
+  p.w_dt = weight_dtype;
+  p.b_dt = bias_dtype;
+  p.i_dt = init_dtype;
+  p.has_bias = bias != nullptr;
+  p.has_init = initial_states != nullptr;
+  p.has_dfinal = dfinal_states != nullptr;
+  p.need_dinit = dinitial_states != nullptr;
+  p.silu = silu != 0;
+
+  p.tl = tl;
+  hipError_t e;
+  if (fast) {
+    switch (x_dtype) {
+      case CCV1D_BF16: e = launch_bwd_fast_t<__bf16>(p, s); break;
+      case CCV1D_F16: e = launch_bwd_fast_t<_Float16>(p, s); break;
+      default: e = launch_bwd_fast_t<float>(p, s); break;
+    }
+  } else {
+    switch (x_dtype) {
+      case CCV1D_BF16: e = launch_bwd_generic_t<__bf16>(p, s); break;
+      case CCV1D_F16: e = launch_bwd_generic_t<_Float16>(p, s); break;
+      case CCV1D_F32: e = launch_bwd_generic_t<float>(p, s); break;
+      default: e = launch_bwd_generic_t<double>(p, s); break;
+    }
+  }
+  if (e != hipSuccess) return hip_fail(e, "backward launch");
+
+  ReduceParams r{};
+  r.part = p.part;
+  r.dw = dweight;
+  r.db = dbias;
+  r.Pn = (int32_t)rows;
+  r.D = (int32_t)D;
+  r.W = (int32_t)W;
+  r.w_dt = weight_dtype;
+  r.b_dt = bias_dtype;
+  r.has_bias = bias != nullptr;
+  e = launch_reduce(r, s);
+  if (e != hipSuccess) return hip_fail(e, "reduce launch");
+  return CCV1D_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,224 @@
+// Scalar kernels for what the vectorised path does not cover: widths above 8, channel counts that
+// are not a multiple of the 16-byte vector, rows that are not 16-byte aligned, and fp64 x. One lane
+// owns one channel of one tile; the lanes of a wave cover 64 consecutive channels, so every row
+// access is still coalesced. Also: the deterministic partial-sum reduction and the small fill/copy
+// kernel used by the empty-sequence paths.
+#pragma once
+
+#include "ccv1d_device.h"
+
+namespace ccv1d {
+
+template <typename TX>
+struct GenRow {
+  const TX* xb;        // x[b, 0, c]
+  int s_xt;
+  const void* initb;   // initial_states[b, 0, c] (byte-offset pointer), or null
+  int i_dt, P, D;
+  // Row `row` (>= -P) of concat(initial_states, x) in fp32 (causal_conv1d.py:28-41).
+  __device__ __forceinline__ float operator()(int row) const {
+    if (row >= 0) return static_cast<float>(xb[row * s_xt]);
+    if (initb) return ld_any(initb, (int64_t)(row + P) * D, i_dt);
+    return 0.0f;
+  }
+};
+
+__device__ __forceinline__ int dt_size(int dt) { return dt == DT_F64 ? 8 : dt == DT_F32 ? 4 : 2; }
+
+// Pre-activation of row t (same operation order as conv_row).
+template <typename TX>
+__device__ __forceinline__ float gen_conv(const GenRow<TX>& xx, const void* w, int w_dt, int c,
+                                          int W, const int32_t* sb, int T, bool has_init, int t,
+                                          int32_t st) {
+  const int P = W - 1;
+  const int64_t wo = (int64_t)c * W;
+  float z = ld_any(w, wo + P, w_dt) * xx(t);
+  for (int k = 0; k < P; ++k) {
+    const int r = t - P + k;
+    if (sb && seq_at(sb, r, T, has_init) != st) continue;
+    z = fmaf(ld_any(w, wo + k, w_dt), xx(r), z);
+  }
+  return z;
+}
+
+template <typename TX>
+__global__ __launch_bounds__(64) void fwd_generic_kernel(const FwdParams p) {
+  const int c = blockIdx.y * 64 + threadIdx.x;
+  if (c >= p.D) return;
+  const int tile = blockIdx.x % p.tl.nT;
+  const int b = blockIdx.x / p.tl.nT;
+  const int T = p.T, D = p.D, W = p.W, P = W - 1;
+  const bool has_init = p.has_init;
+  const int t0 = tile * p.tl.L;
+  const int t1 = min(t0 + p.tl.L, T);
+  GenRow<TX> xx;
+  xx.xb = static_cast<const TX*>(p.x) + (int64_t)b * p.s_xb + c;
+  xx.s_xt = p.s_xt;
+  xx.initb = has_init ? static_cast<const char*>(p.init) + ((int64_t)b * P * D + c) * dt_size(p.i_dt)
+                      : nullptr;
+  xx.i_dt = p.i_dt;
+  xx.P = P;
+  xx.D = D;
+  const int32_t* sb = p.seq ? p.seq + (int64_t)b * T : nullptr;
+  const float bias = p.has_bias ? ld_any(p.bias, c, p.b_dt) : 0.0f;
+  TX* ob = static_cast<TX*>(p.out) + (int64_t)b * T * D + c;
+  const bool silu = p.silu;
+  for (int t = t0; t < t1; ++t) {
+    const int32_t st = sb ? sb[t] : 0;
+    float z = gen_conv(xx, p.w, p.w_dt, c, W, sb, T, has_init, t, st);
+    if (p.has_bias) z += bias;
+    if (sb && st < 0) z = 0.0f;
+    if (silu) z = z * sigmoid_f(z);
+    ob[t * D] = static_cast<TX>(z);
+  }
+  if (p.has_final && t1 == T) {
+    TX* fb = static_cast<TX*>(p.fin) + (int64_t)b * P * D + c;
+    for (int q = 0; q < P; ++q) fb[q * D] = static_cast<TX>(xx(T - P + q));
+  }
+}
+
+// Backward, one lane per channel. The g values of the last W rows live in an LDS ring (one column
+// per lane), as do the dweight accumulators, so the width is a runtime value. Same row semantics
+// and summation structure as bwd_fast_kernel; partial row = b * nT + tile.
+template <typename TX>
+__global__ __launch_bounds__(64) void bwd_generic_kernel(const BwdParams p) {
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x;
+  const int c = blockIdx.y * 64 + lane;
+  if (c >= p.D) return;
+  const int tile = blockIdx.x % p.tl.nT;
+  const int b = blockIdx.x / p.tl.nT;
+  const int T = p.T, D = p.D, W = p.W, P = W - 1;
+  const bool has_init = p.has_init;
+  const bool silu = p.silu;
+  const bool need_dinit = p.need_dinit;
+  float* gring = lds;            // [W][64]: g of rows t-P .. t, slot = row mod W
+  float* dwl = lds + W * 64;     // [W][64]: dweight accumulators
+  for (int k = 0; k < W; ++k) {
+    gring[k * 64 + lane] = 0.0f;
+    dwl[k * 64 + lane] = 0.0f;
+  }
+  float db = 0.0f;
+
+  GenRow<TX> xx;
+  xx.xb = static_cast<const TX*>(p.x) + (int64_t)b * p.s_xb + c;
+  xx.s_xt = p.s_xt;
+  const int isz = dt_size(p.i_dt);
+  xx.initb = has_init ? static_cast<const char*>(p.init) + ((int64_t)b * P * D + c) * isz : nullptr;
+  xx.i_dt = p.i_dt;
+  xx.P = P;
+  xx.D = D;
+  const TX* yb = static_cast<const TX*>(p.dy) + (int64_t)b * p.s_yb + c;
+  TX* dxb = static_cast<TX*>(p.dx) + (int64_t)b * T * D + c;
+  void* dinitb = need_dinit ? static_cast<char*>(p.dinit) + ((int64_t)b * P * D + c) * isz : nullptr;
+  const TX* dfb = p.has_dfinal ? static_cast<const TX*>(p.dfin) + (int64_t)b * P * D + c : nullptr;
+  const int32_t* sb = p.seq ? p.seq + (int64_t)b * T : nullptr;
+  const float bias = p.has_bias ? ld_any(p.bias, c, p.b_dt) : 0.0f;
+  const int64_t wo = (int64_t)c * W;
+
+  const int t0 = tile * p.tl.L;
+  const int own_end = min(t0 + p.tl.L, T);
+  const int t_end = min(own_end + P, T);
+  const int emit_lo = (tile == 0 && need_dinit) ? -P : t0;
+  auto slot = [&](int row) { return ((row % W) + W) % W; };
+
+  // dx of `row` from the g ring (rows row .. row + P), plus dfinal; stores dx or dinit.
+  auto emit = [&](int row) {
+    const int32_t s0 = sb ? seq_at(sb, row, T, has_init) : 0;
+    float dx = ld_any(p.w, wo + P, p.w_dt) * gring[slot(row) * 64 + lane];
+    for (int j = 1; j <= P; ++j) {
+      if (sb && seq_at(sb, row + j, T, has_init) != s0) continue;
+      dx = fmaf(ld_any(p.w, wo + P - j, p.w_dt), gring[slot(row + j) * 64 + lane], dx);
+    }
+    if (dfb) {
+      const int f = row - (T - P);
+      if (f >= 0 && f < P) dx += static_cast<float>(dfb[f * D]);
+    }
+    if (row >= 0) dxb[row * D] = static_cast<TX>(dx);
+    else st_any(dinitb, (int64_t)(row + P) * D, p.i_dt, dx);
+  };
+
+  for (int tt = t0; tt < t_end; ++tt) {
+    const int32_t st = sb ? sb[tt] : 0;
+    float g = static_cast<float>(yb[tt * p.s_yt]);
+    if (silu) {
+      float z = gen_conv(xx, p.w, p.w_dt, c, W, sb, T, has_init, tt, st);
+      if (p.has_bias) z += bias;
+      g = dsilu_times(g, z);
+    }
+    if (sb && st < 0) g = 0.0f;
+    gring[slot(tt) * 64 + lane] = g;
+    if (tt < own_end) {
+      for (int k = 0; k < P; ++k) {
+        const int r = tt - P + k;
+        if (sb && seq_at(sb, r, T, has_init) != st) continue;
+        dwl[k * 64 + lane] = fmaf(g, xx(r), dwl[k * 64 + lane]);
+      }
+      dwl[P * 64 + lane] = fmaf(g, xx(tt), dwl[P * 64 + lane]);
+      db += g;
+    }
+    if (tt - P >= emit_lo) emit(tt - P);
+  }
+  if (t_end == T) {
+    for (int q = 0; q < P; ++q) {
+      gring[slot(T + q) * 64 + lane] = 0.0f;
+      const int row = T + q - P;
+      if (row >= emit_lo && row < own_end) emit(row);
+    }
+  }
+
+  float* pp = p.part + ((int64_t)b * p.tl.nT + tile) * (W + 1) * D + c;
+  for (int k = 0; k < W; ++k) pp[(int64_t)k * D] = dwl[k * 64 + lane];
+  if (p.has_bias) pp[(int64_t)W * D] = db;
+}
+
+// dweight[d, k] = sum_p part[p, k, d] and dbias[d] = sum_p part[p, W, d] (causal_conv1d.py:344-374),
+// in an order fixed by Pn alone: wave w of NWR adds rows w, w + NWR, ... in ascending order, then the
+// NWR wave sums are added in wave order.
+template <int NWR>
+__global__ __launch_bounds__(NWR * 64) void reduce_partials_kernel(const ReduceParams p) {
+  __shared__ float red[NWR][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int K = p.W + (p.has_bias ? 1 : 0);
+  const int64_t N = (int64_t)K * p.D;
+  const int64_t n = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t rs = (int64_t)(p.W + 1) * p.D;
+  float acc = 0.0f;
+  if (n < N) {
+    const float* src = p.part + n;
+    int q = wave;
+    for (; q + 7 * NWR < p.Pn; q += 8 * NWR) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = src[(int64_t)(q + u * NWR) * rs];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; q < p.Pn; q += NWR) acc += src[(int64_t)q * rs];
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && n < N) {
+    float s = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < NWR; ++w) s += red[w][lane];
+    const int k = (int)(n / p.D);
+    const int d = (int)(n % p.D);
+    if (k < p.W) st_any(p.dw, (int64_t)d * p.W + k, p.w_dt, s);
+    else st_any(p.db, d, p.b_dt, s);
+  }
+}
+
+// dst[i] = src[i] converted between element types, or 0 when src is null (used instead of
+// hipMemsetAsync so the paths stay valid inside captured graphs).
+__global__ __launch_bounds__(256) void fill_kernel(void* dst, int dst_dt, const void* src, int src_dt,
+                                                   int64_t n) {
+  const bool same = src && src_dt == dst_dt;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    if (same && dst_dt == DT_F64) static_cast<double*>(dst)[i] = static_cast<const double*>(src)[i];
+    else st_any(dst, i, dst_dt, src ? ld_any(src, i, src_dt) : 0.0f);
+  }
+}
+
+}  // namespace ccv1d

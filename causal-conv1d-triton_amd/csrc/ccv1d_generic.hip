@@ -1,0 +1,46 @@
+// Launchers of the scalar (any width / any alignment) kernels, the partial-sum reduction and the
+// fill kernel.
+#include "ccv1d_generic.h"
+#include "ccv1d_launch.h"
+
+namespace ccv1d {
+
+template <typename TX>
+hipError_t launch_fwd_generic_t(const FwdParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)((int64_t)p.B * p.tl.nT), (unsigned)((p.D + 63) / 64));
+  return launch(reinterpret_cast<const void*>(&fwd_generic_kernel<TX>), grid, dim3(64), 0, s, &p);
+}
+
+template <typename TX>
+hipError_t launch_bwd_generic_t(const BwdParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)((int64_t)p.B * p.tl.nT), (unsigned)((p.D + 63) / 64));
+  const size_t shmem = (size_t)2 * p.W * 64 * sizeof(float);
+  return launch(reinterpret_cast<const void*>(&bwd_generic_kernel<TX>), grid, dim3(64), shmem, s, &p);
+}
+
+template hipError_t launch_fwd_generic_t<float>(const FwdParams&, hipStream_t);
+template hipError_t launch_fwd_generic_t<_Float16>(const FwdParams&, hipStream_t);
+template hipError_t launch_fwd_generic_t<__bf16>(const FwdParams&, hipStream_t);
+template hipError_t launch_fwd_generic_t<double>(const FwdParams&, hipStream_t);
+template hipError_t launch_bwd_generic_t<float>(const BwdParams&, hipStream_t);
+template hipError_t launch_bwd_generic_t<_Float16>(const BwdParams&, hipStream_t);
+template hipError_t launch_bwd_generic_t<__bf16>(const BwdParams&, hipStream_t);
+template hipError_t launch_bwd_generic_t<double>(const BwdParams&, hipStream_t);
+
+hipError_t launch_reduce(const ReduceParams& p, hipStream_t s) {
+  const int64_t n = (int64_t)(p.W + (p.has_bias ? 1 : 0)) * p.D;
+  const dim3 grid((unsigned)((n + 63) / 64));
+  return launch(reinterpret_cast<const void*>(&reduce_partials_kernel<kReduceNW>), grid,
+                dim3(kReduceNW * 64), 0, s, &p);
+}
+
+hipError_t launch_fill(void* dst, int dst_dt, const void* src, int src_dt, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  void* args[] = {&dst, &dst_dt, &src, &src_dt, &n};
+  return hipLaunchKernel(reinterpret_cast<const void*>(&fill_kernel), dim3((unsigned)blocks), dim3(256),
+                         args, 0, s);
+}
+
+}  // namespace ccv1d

@@ -1,0 +1,98 @@
+// Launch helpers: compile-time configuration of the kernels and the dispatch from runtime
+// (width, activation, seq_idx) to template instantiations. Each x dtype's instantiations live in a
+// translation unit of their own (ccv1d_fast_<dtype>.hip) so they compile in parallel.
+#pragma once
+
+#include "ccv1d_device.h"
+
+namespace ccv1d {
+
+constexpr int kFwdNW = 4;        // waves per forward workgroup
+constexpr int kFwdR = 8;         // rows whose loads are issued together (forward)
+constexpr int kBwdNW = 4;        // waves per backward workgroup
+constexpr int kBwdR = 8;         // rows whose loads are issued together (backward)
+constexpr int kMaxFastW = 8;     // widths 2..kMaxFastW have register-window kernels
+constexpr int kMaxGenericW = 128;  // LDS ring of the generic backward: 2 * W * 64 * 4 bytes
+constexpr int kReduceNW = 8;     // waves per reduction workgroup
+constexpr int kGenericL = 64;    // rows per tile of the generic kernels
+
+inline hipError_t launch(const void* kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t s,
+                         const void* params) {
+  void* args[] = {const_cast<void*>(params)};
+  return hipLaunchKernel(kernel, grid, block, args, shmem, s);
+}
+
+template <typename TX>
+hipError_t launch_fwd_fast_t(const FwdParams& p, hipStream_t s);
+template <typename TX>
+hipError_t launch_bwd_fast_t(const BwdParams& p, hipStream_t s);
+template <typename TX>
+hipError_t launch_fwd_generic_t(const FwdParams& p, hipStream_t s);
+template <typename TX>
+hipError_t launch_bwd_generic_t(const BwdParams& p, hipStream_t s);
+hipError_t launch_reduce(const ReduceParams& p, hipStream_t s);
+hipError_t launch_fill(void* dst, int dst_dt, const void* src, int src_dt, int64_t n, hipStream_t s);
+
+}  // namespace ccv1d
+
+#ifdef CCV1D_DEFINE_FAST_LAUNCHERS
+#include "ccv1d_fast.h"
+
+namespace ccv1d {
+
+template <typename TX, int W, bool SILU, bool SEQ>
+static hipError_t fwd_one(const FwdParams& p, hipStream_t s) {
+  return launch(reinterpret_cast<const void*>(&fwd_fast_kernel<TX, W, SILU, SEQ, kFwdNW, kFwdR>),
+                dim3(p.tl.nBlk), dim3(kFwdNW * 64), 0, s, &p);
+}
+
+template <typename TX, int W, bool SILU, bool SEQ>
+static hipError_t bwd_one(const BwdParams& p, hipStream_t s) {
+  return launch(reinterpret_cast<const void*>(&bwd_fast_kernel<TX, W, SILU, SEQ, kBwdNW, kBwdR>),
+                dim3(p.tl.nBlk), dim3(kBwdNW * 64), 0, s, &p);
+}
+
+template <typename TX, int W>
+static hipError_t fwd_w(const FwdParams& p, hipStream_t s) {
+  const bool seq = p.seq != nullptr;
+  if (p.silu) return seq ? fwd_one<TX, W, true, true>(p, s) : fwd_one<TX, W, true, false>(p, s);
+  return seq ? fwd_one<TX, W, false, true>(p, s) : fwd_one<TX, W, false, false>(p, s);
+}
+
+template <typename TX, int W>
+static hipError_t bwd_w(const BwdParams& p, hipStream_t s) {
+  const bool seq = p.seq != nullptr;
+  if (p.silu) return seq ? bwd_one<TX, W, true, true>(p, s) : bwd_one<TX, W, true, false>(p, s);
+  return seq ? bwd_one<TX, W, false, true>(p, s) : bwd_one<TX, W, false, false>(p, s);
+}
+
+template <typename TX>
+hipError_t launch_fwd_fast_t(const FwdParams& p, hipStream_t s) {
+  switch (p.W) {
+    case 2: return fwd_w<TX, 2>(p, s);
+    case 3: return fwd_w<TX, 3>(p, s);
+    case 4: return fwd_w<TX, 4>(p, s);
+    case 5: return fwd_w<TX, 5>(p, s);
+    case 6: return fwd_w<TX, 6>(p, s);
+    case 7: return fwd_w<TX, 7>(p, s);
+    case 8: return fwd_w<TX, 8>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename TX>
+hipError_t launch_bwd_fast_t(const BwdParams& p, hipStream_t s) {
+  switch (p.W) {
+    case 2: return bwd_w<TX, 2>(p, s);
+    case 3: return bwd_w<TX, 3>(p, s);
+    case 4: return bwd_w<TX, 4>(p, s);
+    case 5: return bwd_w<TX, 5>(p, s);
+    case 6: return bwd_w<TX, 6>(p, s);
+    case 7: return bwd_w<TX, 7>(p, s);
+    case 8: return bwd_w<TX, 8>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ccv1d
+#endif

@@ -1,0 +1,122 @@
+/*
+ * ccv1d.h - C ABI of the MI355X (gfx950) causal depthwise conv1d library (libccv1d.so).
+ *
+ * The operation, over channels-last x of shape (batch, seqlen, dim), with P = width - 1:
+ *
+ *   xx[b, t, d]  = x[b, t, d]                 for 0 <= t < seqlen
+ *                = initial_states[b, t+P, d]  for -P <= t < 0 (zero when there are no initial states)
+ *   z[b, t, d]   = weight[d, P] * xx[t] + sum_{k<P} m_k * weight[d, k] * xx[t-P+k]   (fp32)
+ *                  (+ bias[d]); with seq_idx, z = 0 where seq_idx[b, t] < 0
+ *   out[b, t, d] = silu(z) if silu else z, rounded to the x dtype
+ *
+ * where m_k = (seq[t-P+k] == seq[t]) with seq_idx and 1 otherwise; rows t < 0 carry the sequence id of
+ * seq_idx[b, 0] when initial states are given and -1 otherwise.
+ *
+ * Conventions shared by every entry point:
+ *  - All tensor pointers are device pointers on `device`. The caller owns every buffer; the library
+ *    never allocates device memory.
+ *  - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the legacy default stream of
+ *    `device`). The calling thread's current device is restored before returning.
+ *  - x and dout may have arbitrary batch and time strides (in elements) but a unit channel stride.
+ *    Every other tensor is contiguous: weight (dim, width), bias (dim), seq_idx (batch, seqlen) int32,
+ *    initial/final states and their gradients (batch, width - 1, dim), out and dx (batch, seqlen, dim).
+ *  - Offsets inside one batch element are 32-bit: (seqlen + width) * max(x_stride_t, dim) and the same
+ *    for dout must be below 2^31.
+ *  - Return value: CCV1D_OK (0) or an error code; ccv1d_last_error() then describes the failure.
+ *  - Reentrant and thread-safe; the only global state is the error string (thread-local) and a tuning
+ *    table read once from the environment.
+ */
+#ifndef CCV1D_H
+#define CCV1D_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CCV1D_ABI_VERSION 1
+
+/* Element types. x, out, final_states, dout, dfinal_states and dx may be F32, F16 or BF16 (F64 is
+ * accepted on the generic path). weight, bias and initial_states may each have any of the four types;
+ * they are converted to fp32 on load, and their gradients are stored in their own type. */
+enum ccv1d_dtype { CCV1D_F32 = 0, CCV1D_F16 = 1, CCV1D_BF16 = 2, CCV1D_F64 = 3 };
+
+enum ccv1d_status {
+  CCV1D_OK = 0,
+  CCV1D_ERR_INVALID = 1,     /* bad argument: null pointer, negative size, width < 2, bad dtype code */
+  CCV1D_ERR_UNSUPPORTED = 2, /* valid request outside what the kernels implement (e.g. width > 128) */
+  CCV1D_ERR_WORKSPACE = 3,   /* workspace missing or smaller than ccv1d_bwd_workspace_bytes() */
+  CCV1D_ERR_HIP = 4          /* a HIP runtime call or kernel launch failed */
+};
+
+/* Version of this ABI (CCV1D_ABI_VERSION of the built library). */
+int ccv1d_abi_version(void);
+
+/* Description of the last error raised on the calling thread ("" if none). */
+const char* ccv1d_last_error(void);
+
+/* Forward pass. Replaces the host launcher `_fwd` of the reference
+ * (causal_conv1d_triton/causal_conv1d.py:433-472) together with the `_fwd_kernel` it launches
+ * (causal_conv1d.py:44-164) and the empty-input path (causal_conv1d.py:437-444).
+ *
+ *  x                 (batch, seqlen, dim), strides (x_stride_b, x_stride_t, 1), type x_dtype
+ *  weight            (dim, width), type weight_dtype
+ *  bias              (dim,) or NULL, type bias_dtype
+ *  seq_idx           (batch, seqlen) int32 or NULL
+ *  initial_states    (batch, width - 1, dim) or NULL, type init_dtype
+ *  out               (batch, seqlen, dim), type x_dtype
+ *  final_states      (batch, width - 1, dim) or NULL, type x_dtype: the last width - 1 rows of
+ *                    concat(initial_states, x), i.e. the state for continuing the sequence. Must be
+ *                    NULL when seq_idx is given (causal_conv1d.py:607-608).
+ *  silu              0: no activation; 1: out = z * sigmoid(z)
+ */
+int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+              const void* weight, int weight_dtype,
+              const void* bias, int bias_dtype,
+              const int32_t* seq_idx,
+              const void* initial_states, int init_dtype,
+              void* out, void* final_states,
+              int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+              int silu, int device, void* stream);
+
+/* Bytes of device workspace ccv1d_bwd needs for this shape (fp32 partial sums of dweight/dbias; the
+ * reference allocates the same kind of buffer at causal_conv1d.py:493). 0 for empty shapes. */
+size_t ccv1d_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+                                 int x_dtype);
+
+/* Backward pass. Replaces the host launcher `_bwd` of the reference (causal_conv1d.py:475-541)
+ * together with `_bwd_kernel` (causal_conv1d.py:167-341), `_reduce_partials_kernel`
+ * (causal_conv1d.py:344-374) and the empty-input path (causal_conv1d.py:480-489).
+ *
+ *  x, weight, bias, seq_idx, initial_states, silu: as passed to ccv1d_fwd
+ *  dout              (batch, seqlen, dim), strides (dout_stride_b, dout_stride_t, 1), type x_dtype
+ *  dfinal_states     (batch, width - 1, dim) or NULL, type x_dtype: gradient of final_states
+ *  dx                (batch, seqlen, dim), type x_dtype (always written)
+ *  dinitial_states   (batch, width - 1, dim) or NULL, type init_dtype; written when non-NULL, which
+ *                    requires initial_states
+ *  dweight           (dim, width), type weight_dtype (always written)
+ *  dbias             (dim,), type bias_dtype; required iff bias is non-NULL
+ *  workspace         device buffer of at least ccv1d_bwd_workspace_bytes() bytes (256-byte aligned);
+ *                    may be NULL when that size is 0
+ *
+ * dweight and dbias are deterministic: the summation order depends only on the shape.
+ */
+int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+              const void* weight, int weight_dtype,
+              const void* bias, int bias_dtype,
+              const int32_t* seq_idx,
+              const void* initial_states, int init_dtype,
+              const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
+              const void* dfinal_states,
+              void* dx, void* dinitial_states, void* dweight, void* dbias,
+              void* workspace, size_t workspace_bytes,
+              int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+              int silu, int device, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CCV1D_H */

@@ -1,0 +1,111 @@
+"""The C-ABI library without a GPU: it loads next to torch's HIP runtime, exports every entry point
+include/ccv1d.h declares, and rejects invalid requests with the documented status codes before any
+HIP call is made."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+import torch  # noqa: F401  (the library binds to torch's HIP runtime)
+from causal_conv1d_triton import _ffi
+
+_HDR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                    "ccv1d.h")
+
+
+def _header():
+    with open(_HDR) as f:
+        return f.read()
+
+
+def _declared():
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(ccv1d_\w+)\(", _header(),
+                                 flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert _declared() == ["ccv1d_abi_version", "ccv1d_bwd", "ccv1d_bwd_workspace_bytes",
+                           "ccv1d_fwd", "ccv1d_last_error"]
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_ffi.library_path())
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_matches_header():
+    v = int(re.search(r"#define CCV1D_ABI_VERSION (\d+)", _header()).group(1))
+    assert _ffi.load().ccv1d_abi_version() == v
+
+
+def test_workspace_bytes():
+    lib = _ffi.load()
+    assert lib.ccv1d_bwd_workspace_bytes(0, 10, 8, 4, 2) == 0
+    assert lib.ccv1d_bwd_workspace_bytes(1, 0, 8, 4, 2) == 0
+    assert lib.ccv1d_bwd_workspace_bytes(1, 10, 8, 1, 2) == 0
+    n = lib.ccv1d_bwd_workspace_bytes(4, 8192, 1024, 4, 2)
+    # whole fp32 partial rows of (width + 1) * dim floats
+    assert n > 0 and n % (5 * 1024 * 4) == 0
+    # never less than the generic kernel's one partial row per 64-row tile
+    assert n >= 4 * (8192 // 64) * 5 * 1024 * 4
+
+
+def _fwd(lib, **kw):
+    a = dict(x=1 << 20, sxb=0, sxt=8, xdt=2, w=1 << 21, wdt=0, b=None, bdt=0, seq=None, init=None,
+             idt=0, out=1 << 22, fin=None, B=1, T=4, D=8, W=4, silu=1, dev=0, stream=None)
+    a.update(kw)
+    return lib.ccv1d_fwd(a["x"], a["sxb"], a["sxt"], a["xdt"], a["w"], a["wdt"], a["b"], a["bdt"],
+                         a["seq"], a["init"], a["idt"], a["out"], a["fin"], a["B"], a["T"], a["D"],
+                         a["W"], a["silu"], a["dev"], a["stream"])
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(W=1), "width"),
+    (dict(B=-1), "negative"),
+    (dict(xdt=7), "dtype"),
+    (dict(x=None), "x is null"),
+    (dict(w=None), "weight is null"),
+    (dict(out=None), "out is null"),
+    (dict(seq=1 << 23, fin=1 << 24), "final states"),
+    (dict(T=1 << 28, D=16, sxt=16), "2^31"),
+])
+def test_fwd_rejects_invalid_arguments(kw, msg):
+    lib = _ffi.load()
+    assert _fwd(lib, **kw) == 1
+    assert msg in lib.ccv1d_last_error().decode()
+
+
+def test_fwd_empty_batch_is_a_no_op():
+    lib = _ffi.load()
+    assert _fwd(lib, B=0, x=None, out=None) == 0
+    assert lib.ccv1d_last_error().decode() == ""
+
+
+def _bwd(lib, **kw):
+    a = dict(x=1 << 20, xdt=2, w=1 << 21, b=None, init=None, dy=1 << 22, dfin=None, dx=1 << 23,
+             dinit=None, dw=1 << 24, db=None, ws=None, wsb=0, B=1, T=4, D=8, W=4, seq=None)
+    a.update(kw)
+    return lib.ccv1d_bwd(a["x"], 0, 8, a["xdt"], a["w"], 0, a["b"], 0, a["seq"], a["init"], 0,
+                         a["dy"], 0, 8, a["dfin"], a["dx"], a["dinit"], a["dw"], a["db"], a["ws"],
+                         a["wsb"], a["B"], a["T"], a["D"], a["W"], 1, 0, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(db=1 << 25), 1, "dbias"),
+    (dict(b=1 << 25), 1, "dbias"),
+    (dict(dinit=1 << 25), 1, "initial_states"),
+    (dict(dy=None), 1, "dout or dx"),
+    (dict(dw=None), 1, "dweight"),
+    (dict(seq=1 << 25, dfin=1 << 26), 1, "seq_idx"),
+    (dict(ws=None, wsb=0), 3, "workspace"),
+    (dict(ws=1 << 27, wsb=16), 3, "workspace"),
+    (dict(W=200, ws=1 << 27, wsb=1 << 30), 2, "width"),
+])
+def test_bwd_rejects_invalid_arguments(kw, code, msg):
+    # every case fails validation, so no HIP call is reached
+    lib = _ffi.load()
+    assert _bwd(lib, **kw) == code
+    assert msg in lib.ccv1d_last_error().decode()

@@ -1,0 +1,82 @@
+"""The Python boundary without a GPU: import surface, signature and the reference's error behaviour
+(causal_conv1d.py:397-408, :605-610), which all fire before any kernel launch."""
+
+import inspect
+
+import pytest
+import torch
+
+import causal_conv1d_triton
+from causal_conv1d_triton import causal_conv1d_fn
+
+
+def test_import_surface():
+    # causal_conv1d_triton/__init__.py:1-3 of the reference
+    assert causal_conv1d_triton.__all__ == ["causal_conv1d_fn"]
+
+
+def test_signature_matches_reference():
+    # causal_conv1d.py:579-588 of the reference
+    sig = inspect.signature(causal_conv1d_fn)
+    assert list(sig.parameters) == ["x", "weight", "bias", "seq_idx", "initial_states",
+                                    "return_final_states", "final_states_out", "activation"]
+    defaults = {k: v.default for k, v in sig.parameters.items()}
+    assert defaults["bias"] is None and defaults["seq_idx"] is None
+    assert defaults["initial_states"] is None and defaults["final_states_out"] is None
+    assert defaults["return_final_states"] is False and defaults["activation"] is None
+
+
+def _t(B=2, T=8, D=4, W=4):
+    return torch.randn(B, T, D), torch.randn(D, W)
+
+
+def test_bad_activation():
+    x, w = _t()
+    with pytest.raises(NotImplementedError):
+        causal_conv1d_fn(x, w, activation="relu")
+
+
+def test_seq_idx_with_final_states():
+    x, w = _t()
+    with pytest.raises(AssertionError, match="final states"):
+        causal_conv1d_fn(x, w, seq_idx=torch.zeros(2, 8, dtype=torch.int32),
+                         return_final_states=True)
+
+
+def test_final_states_out_requires_return():
+    x, w = _t()
+    with pytest.raises(AssertionError, match="return_final_states"):
+        causal_conv1d_fn(x, w, final_states_out=torch.empty(2, 3, 4))
+
+
+def test_cpu_tensors_rejected():
+    x, w = _t()
+    with pytest.raises(AssertionError):
+        causal_conv1d_fn(x, w)
+
+
+@pytest.mark.parametrize("case", ["x2d", "w_dim", "w1", "bias", "init", "seq"])
+def test_shape_checks(case):
+    x, w = _t()
+    kw = {}
+    if case == "x2d":
+        x = x[0]
+    elif case == "w_dim":
+        w = torch.randn(5, 4)
+    elif case == "w1":
+        w = torch.randn(4, 1)
+    elif case == "bias":
+        kw["bias"] = torch.randn(5)
+    elif case == "init":
+        kw["initial_states"] = torch.randn(2, 2, 4)
+    elif case == "seq":
+        kw["seq_idx"] = torch.zeros(2, 7, dtype=torch.int32)
+    with pytest.raises(AssertionError):
+        causal_conv1d_fn(x, w, **kw)
+
+
+def test_ffi_refuses_unsupported_dtype():
+    from causal_conv1d_triton import _ffi
+
+    with pytest.raises(TypeError):
+        _ffi._code(torch.zeros(1, dtype=torch.int32))

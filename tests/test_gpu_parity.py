@@ -1,0 +1,448 @@
+"""GPU parity: the HIP kernels (through causal_conv1d_fn -> libccv1d.so) against the C oracle on
+identical seeded inputs, plus the invariants that must hold bit for bit.
+
+Tolerances (from the build's north star):
+  * bf16/fp16 out, dx, dinit: |gpu - ref| <= 1e-2 + 1e-2 |ref|, ref = the oracle's fp32 value. The
+    kernels evaluate every output in the oracle's operation order, so without an activation the
+    results are also required to be bit-identical to the oracle rounded to the output dtype, and
+    with silu at least 99% of them must be (the exp/reciprocal implementations differ by ulps).
+  * fp32 out, dx, dinit: |gpu - ref| <= 1e-5 + 1e-5 |ref|.
+  * dweight, dbias (fp32): |gpu - ref| <= 1e-3 |ref| + 1e-3 rms(ref), ref summed in double.
+    In a bf16/fp16 parameter dtype the result is rounded, so 1e-2 replaces 1e-3.
+  * Bit-exact: padding positions give out == 0 and dx == 0, final_states == the last width-1 rows
+    of concat(initial_states, x), chunked forward == full forward, repeated backward gives the same
+    dweight/dbias bits.
+BASELINE configurations 2-5 run at full size; the oracle (single-threaded C) checks a subset of
+channels there, which is exact because channels never interact in a depthwise convolution.
+"""
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import ccv1d_oracle as oracle
+from causal_conv1d_triton import causal_conv1d_fn
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def make_inputs(seed, B, T, D, W, xdt=torch.bfloat16, wdt=torch.float32, bias=True, init=False,
+                idt=None, seq=None, wdist="normal"):
+    g = _gen(seed)
+    inp = {"B": B, "T": T, "D": D, "W": W}
+    inp["x"] = torch.randn(B, T, D, generator=g).to(xdt)
+    if wdist == "uniform":
+        inp["w"] = (torch.rand(D, W, generator=g) - 0.5).to(wdt)
+        inp["b"] = ((torch.rand(D, generator=g) - 0.5) * 0.2).to(wdt) if bias else None
+    else:
+        inp["w"] = (torch.randn(D, W, generator=g) / math.sqrt(W)).to(wdt)
+        inp["b"] = torch.randn(D, generator=g).to(wdt) if bias else None
+    inp["init"] = torch.randn(B, W - 1, D, generator=g).to(idt or xdt) if init else None
+    inp["dy"] = torch.randn(B, T, D, generator=g).to(xdt)
+    inp["dfinal"] = torch.randn(B, W - 1, D, generator=g).to(xdt)
+    inp["seq"] = seq
+    return inp
+
+
+def varlen_seq(seed, B, T, lo=64, hi=4096, pad_frac=0.05):
+    """Consecutive segments with lengths ~U[lo, hi] and ids 0, 1, 2, ...; last pad_frac is -1."""
+    g = _gen(seed)
+    s = torch.empty(B, T, dtype=torch.int32)
+    for b in range(B):
+        t, sid = 0, 0
+        while t < T:
+            n = int(torch.randint(lo, hi + 1, (1,), generator=g))
+            s[b, t:t + n] = sid
+            t += n
+            sid += 1
+        s[b, T - int(pad_frac * T):] = -1
+    return s
+
+
+def _np32(t):
+    return None if t is None else t.float().numpy()
+
+
+def _sub(t, cols, dim=-1):
+    return None if t is None else t.index_select(dim, cols)
+
+
+def oracle_ref(inp, silu, cols=None, final=False, dfinal=False, need_dinit=False, bwd=True):
+    """Oracle outputs (fp32 numpy; dweight/dbias float64) for all channels or the subset `cols`."""
+    x, w, b, init, dy, df = inp["x"], inp["w"], inp["b"], inp["init"], inp["dy"], inp["dfinal"]
+    if cols is not None:
+        x, dy = _sub(x, cols), _sub(dy, cols)
+        init, df = _sub(init, cols), _sub(df, cols)
+        w, b = _sub(w, cols, 0), _sub(b, cols, 0)
+    seq = None if inp["seq"] is None else inp["seq"].numpy()
+    r = {}
+    r["out"], r["final"] = oracle.fwd(_np32(x), _np32(w), _np32(b), seq, _np32(init), silu=silu,
+                                      final=final)
+    if bwd:
+        r["dx"], r["dinit"], r["dw"], r["db"] = oracle.bwd(
+            _np32(x), _np32(w), _np32(dy), _np32(b), seq, _np32(init),
+            _np32(df) if dfinal else None, need_dinit=need_dinit, silu=silu)
+    return r
+
+
+def run_gpu(inp, activation, return_final=False, dfinal=False, init_grad=False, bwd=True,
+            x_override=None):
+    x = (x_override if x_override is not None else inp["x"].to(DEV)).detach().requires_grad_(bwd)
+    w = inp["w"].to(DEV).requires_grad_(bwd)
+    b = inp["b"].to(DEV).requires_grad_(bwd) if inp["b"] is not None else None
+    init = inp["init"].to(DEV).requires_grad_(init_grad) if inp["init"] is not None else None
+    seq = inp["seq"].to(DEV) if inp["seq"] is not None else None
+    res = causal_conv1d_fn(x, w, b, seq_idx=seq, initial_states=init,
+                           return_final_states=return_final, activation=activation)
+    out, fin = res if return_final else (res, None)
+    r = {"out": out.detach().cpu(), "final": None if fin is None else fin.detach().cpu()}
+    if bwd:
+        loss = (out.float() * inp["dy"].to(DEV).float()).sum()
+        if return_final and dfinal:
+            loss = loss + (fin.float() * inp["dfinal"].to(DEV).float()).sum()
+        loss.backward()
+        r["dx"] = x.grad.cpu()
+        r["dw"] = w.grad.cpu()
+        r["db"] = None if b is None else b.grad.cpu()
+        r["dinit"] = None if init is None or not init_grad else init.grad.cpu()
+    torch.cuda.synchronize()
+    return r
+
+
+def check_lowp(gpu, ref32, exact, what):
+    """bf16/fp16/fp32 values vs the oracle's fp32 values (see the module docstring)."""
+    ref = torch.from_numpy(np.ascontiguousarray(ref32))
+    if gpu.dtype == torch.float32:
+        torch.testing.assert_close(gpu, ref, rtol=1e-5, atol=1e-5, msg=what)
+        return
+    if gpu.dtype == torch.float64:
+        torch.testing.assert_close(gpu, ref.double(), rtol=1e-5, atol=1e-5, msg=what)
+        return
+    torch.testing.assert_close(gpu.float(), ref, rtol=1e-2, atol=1e-2, msg=what)
+    same = (gpu == ref.to(gpu.dtype)) | (gpu.isnan() & ref.to(gpu.dtype).isnan())
+    frac = same.float().mean().item() if same.numel() else 1.0
+    if exact:
+        assert frac == 1.0, f"{what}: {1 - frac:.2e} of values differ from the oracle's rounding"
+    else:
+        assert frac >= 0.99, f"{what}: only {frac:.4f} of values match the oracle's rounding"
+
+
+def check_sum(gpu, ref64, what):
+    ref = torch.from_numpy(np.ascontiguousarray(ref64))
+    tol = 1e-3 if gpu.dtype in (torch.float32, torch.float64) else 1e-2
+    rms = ref.pow(2).mean().sqrt().item() if ref.numel() else 0.0
+    torch.testing.assert_close(gpu.double(), ref, rtol=tol, atol=tol * rms + 1e-6, msg=what)
+
+
+def compare(gpu, ref, silu, cols=None):
+    pick = (lambda t: t) if cols is None else (lambda t: None if t is None else _sub(t, cols))
+    exact = not silu
+    check_lowp(pick(gpu["out"]), ref["out"], exact, "out")
+    if gpu.get("final") is not None and ref.get("final") is not None:
+        assert torch.equal(pick(gpu["final"]).float(), torch.from_numpy(ref["final"])), "final"
+    if "dx" in gpu and "dx" in ref:
+        check_lowp(pick(gpu["dx"]), ref["dx"], exact, "dx")
+        w_sub = gpu["dw"] if cols is None else _sub(gpu["dw"], cols, 0)
+        check_sum(w_sub, ref["dw"], "dweight")
+        if gpu["db"] is not None:
+            b_sub = gpu["db"] if cols is None else _sub(gpu["db"], cols, 0)
+            check_sum(b_sub, ref["db"], "dbias")
+        if gpu.get("dinit") is not None:
+            check_lowp(pick(gpu["dinit"]), ref["dinit"], exact, "dinit")
+
+
+def test_native_library_is_loaded():
+    inp = make_inputs(0, 1, 16, 64, 4)
+    run_gpu(inp, "silu")
+    with open("/proc/self/maps") as f:
+        maps = f.read()
+    assert "libccv1d.so" in maps
+
+
+def test_readme_example():
+    """x (2,1024,512) bf16 ~N(0,1), weight (512,4) fp32 ~N(0,1), bias (512)
+    fp32 ~N(0,1), silu, out.sum().backward(); seed 0."""
+    g = _gen(0)
+    x = torch.randn(2, 1024, 512, generator=g).to(torch.bfloat16)
+    w = torch.randn(512, 4, generator=g)
+    b = torch.randn(512, generator=g)
+    inp = {"x": x, "w": w, "b": b, "init": None, "seq": None, "dfinal": None,
+           "dy": torch.ones(2, 1024, 512, dtype=torch.bfloat16)}
+    gpu = run_gpu(inp, "silu")
+    compare(gpu, oracle_ref(inp, True), True)
+
+
+@pytest.mark.parametrize("W", [2, 3, 4, 5, 7, 9])
+@pytest.mark.parametrize("act", [None, "silu"])
+def test_widths_and_lengths(W, act):
+    P = W - 1
+    for T in sorted({1, max(1, P - 1), P, P + 1, 17, 1000}):
+        for D in (8, 1024):
+            inp = make_inputs(1000 * W + T + D, 2, T, D, W, bias=act is not None, init=T % 2 == 1)
+            gpu = run_gpu(inp, act, return_final=True, dfinal=True, init_grad=True)
+            ref = oracle_ref(inp, act is not None, final=True, dfinal=True,
+                             need_dinit=inp["init"] is not None)
+            compare(gpu, ref, act is not None)
+
+
+@pytest.mark.parametrize("D", [1, 7, 1000, 5376])
+def test_channel_counts(D):
+    inp = make_inputs(D, 2, 300, D, 4, init=True)
+    gpu = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=True)
+    compare(gpu, oracle_ref(inp, True, final=True, dfinal=True, need_dinit=True), True)
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize("wdt", [torch.float32, torch.bfloat16])
+def test_dtypes(xdt, wdt):
+    inp = make_inputs(7, 2, 257, 256, 4, xdt=xdt, wdt=wdt, init=True, idt=torch.float32)
+    gpu = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=True)
+    assert gpu["out"].dtype == xdt and gpu["dx"].dtype == xdt
+    assert gpu["dw"].dtype == wdt and gpu["db"].dtype == wdt and gpu["dinit"].dtype == torch.float32
+    compare(gpu, oracle_ref(inp, True, final=True, dfinal=True, need_dinit=True), True)
+
+
+@pytest.mark.parametrize("layout", ["time_stride", "aligned_slice", "misaligned_slice"])
+def test_strided_x_and_dout(layout):
+    B, T, D, W = 2, 500, 256, 4
+    inp = make_inputs(11, B, T, D, W, init=True)
+    if layout == "time_stride":
+        big = torch.zeros(B, 2 * T, D, dtype=torch.bfloat16)
+        big[:, ::2] = inp["x"]
+        xg = big.to(DEV)[:, ::2]
+    else:
+        off = 64 if layout == "aligned_slice" else 3
+        big = torch.zeros(B, T, D + 72, dtype=torch.bfloat16)
+        big[..., off:off + D] = inp["x"]
+        xg = big.to(DEV)[..., off:off + D]
+    assert xg.stride(-1) == 1 and not xg.is_contiguous()
+    x = xg.detach().requires_grad_(True)
+    w = inp["w"].to(DEV).requires_grad_(True)
+    b = inp["b"].to(DEV).requires_grad_(True)
+    init = inp["init"].to(DEV).requires_grad_(True)
+    out = causal_conv1d_fn(x, w, b, initial_states=init, activation="silu")
+    dyb = torch.zeros(B, 2 * T, D, dtype=torch.bfloat16, device=DEV)
+    dyb[:, ::2] = inp["dy"].to(DEV)
+    out.backward(dyb[:, ::2])
+    gpu = {"out": out.detach().cpu(), "dx": x.grad.cpu(), "dw": w.grad.cpu(), "db": b.grad.cpu(),
+           "dinit": init.grad.cpu()}
+    compare(gpu, oracle_ref(inp, True, need_dinit=True), True)
+
+
+@pytest.mark.parametrize("W", [2, 4, 7])
+@pytest.mark.parametrize("init", [False, True])
+def test_seq_idx(W, init):
+    B, T, D = 3, 2000, 512
+    seq = varlen_seq(W, B, T, lo=16, hi=400, pad_frac=0.05)
+    seq[1, 100:140] = -7           # negative ids other than -1 are padding too
+    seq[2, 300:350] = 0            # a later segment reusing an earlier id still connects
+    inp = make_inputs(W + 10 * init, B, T, D, W, init=init, seq=seq)
+    gpu = run_gpu(inp, "silu", init_grad=init)
+    ref = oracle_ref(inp, True, need_dinit=init)
+    compare(gpu, ref, True)
+    pad = seq < 0
+    assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0)
+
+
+def test_seq_idx_int64_and_all_equal():
+    B, T, D, W = 2, 300, 128, 4
+    inp = make_inputs(3, B, T, D, W, init=True)
+    base = run_gpu(inp, "silu", init_grad=True)
+    inp_eq = dict(inp, seq=torch.full((B, T), 5, dtype=torch.int64))
+    same = run_gpu(inp_eq, "silu", init_grad=True)
+    assert torch.equal(base["out"], same["out"]) and torch.equal(base["dx"], same["dx"])
+    assert torch.equal(base["dinit"], same["dinit"])
+
+
+def test_state_handoff_bit_exact():
+    B, T, D, W = 3, 1000, 512, 4
+    inp = make_inputs(5, B, T, D, W, init=True)
+    x = inp["x"].to(DEV)
+    w, b, init = inp["w"].to(DEV), inp["b"].to(DEV), inp["init"].to(DEV)
+    with torch.no_grad():
+        full, fin = causal_conv1d_fn(x, w, b, initial_states=init, return_final_states=True,
+                                     activation="silu")
+        xx = torch.cat([init, x], dim=1)
+        assert torch.equal(fin, xx[:, T:])
+        state, outs = init, []
+        for lo, hi in ((0, 1), (1, 3), (3, 400), (400, 999), (999, 1000)):
+            o, state = causal_conv1d_fn(x[:, lo:hi], w, b, initial_states=state,
+                                        return_final_states=True, activation="silu")
+            outs.append(o)
+        assert torch.equal(torch.cat(outs, dim=1), full)
+        assert torch.equal(state, fin)
+        buf = torch.empty_like(fin)
+        o2, f2 = causal_conv1d_fn(x, w, b, initial_states=init, return_final_states=True,
+                                  final_states_out=buf, activation="swish")
+        assert f2 is buf and torch.equal(buf, fin) and torch.equal(o2, full)
+
+
+def test_deterministic_weight_grads():
+    inp = make_inputs(9, 4, 4096, 1024, 4)
+    a = run_gpu(inp, "silu")
+    b = run_gpu(inp, "silu")
+    assert torch.equal(a["dw"], b["dw"]) and torch.equal(a["db"], b["db"])
+    assert torch.equal(a["dx"], b["dx"])
+
+
+def test_init_without_grad_and_no_grad_inputs():
+    inp = make_inputs(4, 2, 100, 64, 4, init=True)
+    gpu = run_gpu(inp, "silu", init_grad=False)
+    assert gpu["dinit"] is None
+    compare(gpu, oracle_ref(inp, True), True)
+    with torch.no_grad():
+        out = causal_conv1d_fn(inp["x"].to(DEV), inp["w"].to(DEV), inp["b"].to(DEV),
+                               initial_states=inp["init"].to(DEV), activation="silu")
+    check_lowp(out.cpu(), oracle_ref(inp, True, bwd=False)["out"], False, "no-grad out")
+
+
+@pytest.mark.parametrize("shape", [(2, 0, 64), (0, 10, 64), (2, 10, 0)])
+def test_empty_inputs(shape):
+    B, T, D = shape
+    W = 4
+    inp = make_inputs(1, B, T, D, W, init=True)
+    x = inp["x"].to(DEV).requires_grad_(True)
+    w = inp["w"].to(DEV).requires_grad_(True)
+    b = inp["b"].to(DEV).requires_grad_(True)
+    init = inp["init"].to(DEV).requires_grad_(True)
+    out, fin = causal_conv1d_fn(x, w, b, initial_states=init, return_final_states=True,
+                                activation="silu")
+    assert out.shape == (B, T, D)
+    assert torch.equal(fin, init.detach())  # with T == 0 the final states are the initial states
+    dfin = inp["dfinal"].to(DEV)
+    (out.float().sum() + (fin.float() * dfin.float()).sum()).backward()
+    assert torch.equal(w.grad, torch.zeros_like(w)) and torch.equal(b.grad, torch.zeros_like(b))
+    if T == 0:
+        assert torch.equal(init.grad, dfin.to(init.dtype))
+
+
+def test_width_limit_error():
+    from causal_conv1d_triton._ffi import CCV1DError
+
+    x = torch.randn(1, 8, 16, device=DEV)
+    w = torch.randn(16, 200, device=DEV)
+    with pytest.raises(CCV1DError, match="width"):
+        causal_conv1d_fn(x, w)
+
+
+# ------------------------------------------------------------------------------------------------
+# BASELINE configurations at full size.
+# ------------------------------------------------------------------------------------------------
+
+def _cols(D, n, seed):
+    g = _gen(seed)
+    idx = torch.randperm(D, generator=g)[:n]
+    return torch.cat([idx, torch.tensor([0, D - 1])]).unique()
+
+
+@pytest.mark.parametrize("T", [512, 2048, 8192, 32768])
+@pytest.mark.parametrize("variant", ["weight_only", "bias_silu"])
+def test_config2_readme_sweep(T, variant):
+    """B=4, D=1024, W=4, bf16 x, fp32 weight ~N(0, 1/4); weight only, or bias ~N(0,1) + silu."""
+    bias = variant == "bias_silu"
+    inp = make_inputs(T, 4, T, 1024, 4, bias=bias)
+    act = "silu" if bias else None
+    gpu = run_gpu(inp, act)
+    cols = _cols(1024, 30, T)
+    compare(gpu, oracle_ref(inp, bias, cols=cols), bias, cols=cols)
+
+
+def test_config3_mamba2_xbc():
+    """B=8, T=4096, D=5376, W=4; x a channel slice of an in_proj output (time stride 10576)."""
+    B, T, D, W = 8, 4096, 5376, 4
+    inp = make_inputs(3, B, T, D, W, wdist="uniform")
+    big = torch.empty(B, T, 10576, dtype=torch.bfloat16, device=DEV)
+    big[..., 5120:5120 + D] = inp["x"].to(DEV)
+    gpu = run_gpu(inp, "silu", x_override=big[..., 5120:5120 + D])
+    cols = _cols(D, 24, 3)
+    compare(gpu, oracle_ref(inp, True, cols=cols), True, cols=cols)
+
+
+def test_config4_streaming_chunks_and_decode():
+    """B=16, D=2048, W=4, T=8192 as 32 chunks of 256 with state handoff, and 64 decode steps of
+    T=1: both bit-identical to one full-length pass."""
+    B, T, D, W = 16, 8192, 2048, 4
+    inp = make_inputs(4, B, T, D, W)
+    x, w, b = inp["x"].to(DEV), inp["w"].to(DEV), inp["b"].to(DEV)
+    with torch.no_grad():
+        full, fin = causal_conv1d_fn(x, w, b, return_final_states=True, activation="silu")
+        state, outs = None, []
+        for c in range(32):
+            o, state = causal_conv1d_fn(x[:, c * 256:(c + 1) * 256], w, b, initial_states=state,
+                                        return_final_states=True, activation="silu")
+            outs.append(o)
+        assert torch.equal(torch.cat(outs, dim=1), full)
+        assert torch.equal(state, fin)
+        state = None
+        for t in range(64):
+            o, state = causal_conv1d_fn(x[:, t:t + 1], w, b, initial_states=state,
+                                        return_final_states=True, activation="silu")
+            assert torch.equal(o, full[:, t:t + 1]), t
+    cols = _cols(D, 16, 4)
+    ref = oracle_ref(inp, True, cols=cols, final=True, bwd=False)
+    check_lowp(_sub(full.cpu(), cols), ref["out"], False, "full out")
+    assert torch.equal(_sub(fin.cpu(), cols).float(), torch.from_numpy(ref["final"]))
+
+
+def test_config4_chunked_training_matches_full():
+    """Gradients through the state handoff: two chunks vs one pass (tolerance only, since the
+    state gradient is rounded to bf16 between the chunks)."""
+    B, T, D, W = 4, 1024, 512, 4
+    inp = make_inputs(8, B, T, D, W)
+    x = inp["x"].to(DEV).requires_grad_(True)
+    w = inp["w"].to(DEV).requires_grad_(True)
+    b = inp["b"].to(DEV).requires_grad_(True)
+    dy = inp["dy"].to(DEV)
+    out = causal_conv1d_fn(x, w, b, activation="silu")
+    (out.float() * dy.float()).sum().backward()
+    g_full = [t.grad.clone() for t in (x, w, b)]
+    for t in (x, w, b):
+        t.grad = None
+    o1, s1 = causal_conv1d_fn(x[:, :400], w, b, return_final_states=True, activation="silu")
+    o2 = causal_conv1d_fn(x[:, 400:], w, b, initial_states=s1, activation="silu")
+    assert torch.equal(torch.cat([o1, o2], dim=1), out)
+    (torch.cat([o1, o2], dim=1).float() * dy.float()).sum().backward()
+    torch.testing.assert_close(x.grad.float(), g_full[0].float(), rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(w.grad, g_full[1], rtol=1e-3, atol=1e-2)
+    torch.testing.assert_close(b.grad, g_full[2], rtol=1e-3, atol=1e-2)
+
+
+@pytest.mark.parametrize("W", [4, 7])
+def test_config5_varlen_seq_idx(W):
+    """B=4, T=16384, D=4096; segments ~U[64,4096] with ids 0,1,2,... and the last 5% padding (-1);
+    initial_states bf16 belong to segment 0; bias + silu, forward + backward."""
+    B, T, D = 4, 16384, 4096
+    seq = varlen_seq(50 + W, B, T)
+    inp = make_inputs(W, B, T, D, W, init=True, seq=seq)
+    gpu = run_gpu(inp, "silu", init_grad=True)
+    pad = seq < 0
+    assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0)
+    cols = _cols(D, 12, W)
+    compare(gpu, oracle_ref(inp, True, cols=cols, need_dinit=True), True, cols=cols)
+
+
+def test_maximum_in_batch_offset():
+    """(T + W) * D just below 2^31: the largest sequence the 32-bit in-batch offsets allow."""
+    D, W = 2048, 4
+    T = (2**31 - 1) // D - W
+    g = torch.Generator(DEV).manual_seed(12)
+    x = torch.randn(1, T, D, generator=g, device=DEV, dtype=torch.bfloat16)
+    w = torch.randn(D, W, generator=g, device=DEV) / 2
+    with torch.no_grad():
+        out, fin = causal_conv1d_fn(x, w, return_final_states=True)
+    cols = torch.tensor([0, 1, 777, D - 1])
+    xs = _sub(x, cols.to(DEV)).cpu()
+    ws = _sub(w, cols.to(DEV), 0).cpu()
+    del x
+    ref, rfin = oracle.fwd(_np32(xs), _np32(ws), final=True)
+    check_lowp(_sub(out.cpu(), cols), ref, True, "out")
+    assert torch.equal(_sub(fin.cpu(), cols).float(), torch.from_numpy(rfin))

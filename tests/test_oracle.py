@@ -1,0 +1,88 @@
+"""Pins the C oracle (oracle/ccv1d_oracle.c) before it is trusted as the GPU checker: float64
+closed forms (grouped F.conv1d and its autograd), the shifted-sum form with sequence masks,
+per-element brute force, committed known-answer vectors, textbook special cases and bit-exact
+invariants (state handoff, padding, seq special cases). CPU only."""
+
+import pytest
+
+import pins
+
+WIDTHS = [2, 3, 4, 5, 7, 9]
+
+
+def _lengths(W):
+    P = W - 1
+    return sorted({1, max(1, P - 1), P, P + 1, 17, 120})
+
+
+@pytest.mark.parametrize("W", WIDTHS)
+@pytest.mark.parametrize("variant", ["plain", "bias_silu", "init_bias_silu", "init_dfinal_noact"])
+def test_fwd_bwd_vs_closed_form(W, variant):
+    for T in _lengths(W):
+        c = pins.make_case(
+            seed=100 * W + T, B=2, T=T, D=7, W=W,
+            bias=variant != "plain",
+            init="init" in variant,
+            dfinal="dfinal" in variant,
+            silu="silu" in variant,
+        )
+        ok, det = pins.check_fwd_closed_form(c)
+        assert ok, f"T={T}: {det}"
+        ok, det = pins.check_bwd_autograd(c)
+        assert ok, f"T={T}: {det}"
+
+
+@pytest.mark.parametrize("W", [2, 4, 7])
+@pytest.mark.parametrize("seq", ["segments", "padded"])
+@pytest.mark.parametrize("init", [False, True])
+def test_seq_vs_shifted_form(W, seq, init):
+    for T in (1, W, 33, 200):
+        c = pins.make_case(seed=7 * W + T, B=3, T=T, D=5, W=W, init=init, seq=seq, silu=True)
+        ok, det = pins.check_fwd_shifted(c)
+        assert ok, f"T={T}: {det}"
+        ok, det = pins.check_bwd_autograd(c)
+        assert ok, f"T={T}: {det}"
+
+
+@pytest.mark.parametrize("W", [2, 3, 4, 6])
+@pytest.mark.parametrize("seq", [None, "padded"])
+@pytest.mark.parametrize("silu", [False, True])
+def test_brute_force_tiny(W, seq, silu):
+    for T in (1, W - 1, W + 2, 9):
+        T = max(T, 1)
+        c = pins.make_case(seed=31 * W + T, B=2, T=T, D=3, W=W, init=True, seq=seq,
+                           dfinal=seq is None, silu=silu)
+        ok, det = pins.check_brute(c)
+        assert ok, f"T={T}: {det}"
+
+
+@pytest.mark.parametrize("k", pins.kat_cases(), ids=lambda k: k["name"])
+def test_known_answers(k):
+    ok, det = pins.check_kat(k)
+    assert ok, det
+
+
+@pytest.mark.parametrize("W", [2, 4, 5])
+@pytest.mark.parametrize("silu", [False, True])
+def test_seq_special_cases(W, silu):
+    c = pins.make_case(seed=W, B=2, T=50, D=6, W=W, init=True, silu=silu)
+    ok, det = pins.check_seq_special(c)
+    assert ok, det
+
+
+@pytest.mark.parametrize("W", [2, 4, 9])
+@pytest.mark.parametrize("init", [False, True])
+def test_state_handoff(W, init):
+    for T, split in ((40, 17), (40, 1), (W - 1, 1), (2 * W, W)):
+        if split >= T:
+            continue
+        c = pins.make_case(seed=T + W, B=2, T=T, D=5, W=W, init=init, silu=True)
+        ok, det = pins.check_state_handoff(c, split)
+        assert ok, f"T={T} split={split}: {det}"
+
+
+@pytest.mark.parametrize("W", [2, 4, 7])
+def test_textbook_without_activation(W):
+    c = pins.make_case(seed=W, B=3, T=64, D=9, W=W, init=True, dfinal=True, silu=False)
+    ok, det = pins.check_textbook_no_act(c)
+    assert ok, det
