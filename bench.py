@@ -6,8 +6,8 @@ bias (1024) fp32 ~N(0,1), activation silu, upstream gradient (4, 8192, 1024) bf1
 out = causal_conv1d_fn(x, w, b, activation="silu") followed by the gradients of x, w and b
 (torch.autograd.grad, so nothing is accumulated). Input sets rotate (4 sets of x and dy, 512 MiB, twice
 the 256 MiB Infinity Cache) so every step reads its inputs from HBM. Steps are captured once per input
-set in a HIP graph and replayed, which removes Python launch overhead from the device timeline; the
-eager (un-captured) rate is reported beside it.
+set into one HIP graph (a replay runs one step per input set back to back) and replayed, which removes
+Python launch overhead from the device timeline; the eager (un-captured) rate is reported beside it.
 
 Prints one JSON line. `value` is the step's algorithmic HBM bytes (read x, write out; read x, read dy,
 write dx; plus weights and bias) divided by the measured step time, in GB/s.
@@ -51,18 +51,19 @@ def _capture(fn, warm_stream):
     return g
 
 
-def _time_graphs(graphs, steps, warmup):
-    for k in range(warmup):
-        graphs[k % len(graphs)].replay()
+def _time_graphs(seq, warmup):
+    """Device time of replaying the graphs in `seq` in order (events around the whole sequence)."""
+    for g in seq[:warmup]:
+        g.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
-    for k in range(steps):
-        graphs[k % len(graphs)].replay()
+    for g in seq:
+        g.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    return start.elapsed_time(end)
 
 
 def cpu_baseline(seconds):
@@ -137,20 +138,26 @@ def main():
         out = causal_conv1d_fn(x, w, b, activation="silu")
         return torch.autograd.grad(out, (x, w, b), dy)
 
+    # One graph holds one step per input set, so a replay is len(sets) steps back to back and the
+    # per-replay launch cost is amortised over them; single-step graphs make up any remainder, so
+    # exactly args.steps steps are timed.
     side = torch.cuda.Stream()
     results = []
-    step_graphs = [_capture(lambda i=i: results.append(step(i)), side) for i in range(args.sets)]
+    all_sets = _capture(lambda: results.extend(step(i) for i in range(args.sets)), side)
+    single = [_capture(lambda i=i: results.extend(step(i)), side) for i in range(args.sets)]
     results.clear()
-    ms_step = _time_graphs(step_graphs, args.steps, args.warmup)
+    seq = [all_sets] * (args.steps // args.sets) + single[:args.steps % args.sets]
+    _time_graphs([all_sets] * max(1, args.warmup // args.sets), 0)
+    ms_step = _time_graphs(seq, 0) / args.steps
 
-    # Per-pass device time of the two launches that make up a step, each captured on its own.
-    fwd_graphs = [_capture(lambda i=i: _fwd(sets[i][0].detach(), w.detach(), b.detach(), None,
-                                            None, None, True), side) for i in range(args.sets)]
-    bwd_graphs = [_capture(lambda i=i: _bwd(sets[i][0].detach(), w.detach(), b.detach(), None,
-                                            None, sets[i][1], None, False, True), side)
-                  for i in range(args.sets)]
-    ms_fwd = _time_graphs(fwd_graphs, args.steps, args.warmup)
-    ms_bwd = _time_graphs(bwd_graphs, args.steps, args.warmup)
+    # Per-pass device time of the launches that make up a step, each pass captured on its own.
+    fwd_graph = _capture(lambda: [_fwd(x.detach(), w.detach(), b.detach(), None, None, None, True)
+                                  for x, _ in sets], side)
+    bwd_graph = _capture(lambda: [_bwd(x.detach(), w.detach(), b.detach(), None, None, dy, None,
+                                       False, True) for x, dy in sets], side)
+    reps = max(1, args.steps // args.sets)
+    ms_fwd = _time_graphs([fwd_graph] * reps, 2) / (reps * args.sets)
+    ms_bwd = _time_graphs([bwd_graph] * reps, 2) / (reps * args.sets)
 
     eager_ms = None
     if not args.no_eager:
@@ -185,7 +192,8 @@ def main():
             "workload": "causal_conv1d_fn fwd+bwd, bias+silu (BASELINE configs[1] at T=8192)",
             "batch": B, "seqlen": T, "dim": D, "width": W,
             "x_dtype": "bf16", "weight_dtype": "fp32", "input_sets": args.sets,
-            "timing": "hip graph replay per input set, events around the timed steps",
+            "timing": "one hip graph of one step per input set, replayed; events around the "
+                      "timed replays",
         },
         "passes_us": {"fwd": round(ms_fwd * 1e3, 2), "bwd": round(ms_bwd * 1e3, 2)},
         "eager_ms_per_step": None if eager_ms is None else round(eager_ms, 4),

@@ -34,9 +34,21 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 bool valid_dt(int dt) { return dt >= CCV1D_F32 && dt <= CCV1D_F64; }
 
-int vec_of(int x_dt) { return x_dt == CCV1D_F32 ? 4 : 8; }  // 16-byte vectors
+int esize(int dt) { return dt == CCV1D_F64 ? 8 : dt == CCV1D_F32 ? 4 : 2; }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+// Channels per lane and waves per workgroup of the vectorised kernels for an x dtype.
+struct FastShape {
+  int cpl, nw;
+};
+
+template <template <typename> class Cfg>
+FastShape shape_of(int x_dt) {
+  switch (x_dt) {
+    case CCV1D_BF16: return {Cfg<__bf16>::CPL, Cfg<__bf16>::NW};
+    case CCV1D_F16: return {Cfg<_Float16>::CPL, Cfg<_Float16>::NW};
+    default: return {Cfg<float>::CPL, Cfg<float>::NW};
+  }
+}
 
 // Row tiling overrides for tuning sweeps, read once: CCV1D_FWD_ROWS / CCV1D_BWD_ROWS (rows per tile
 // of the vectorised kernels; a power of two in [8, 1024]).
@@ -83,11 +95,13 @@ Tiling fast_tiling(int64_t B, int64_t T, int64_t D, int vec, int nw, int lmin, i
 }
 
 Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
-  return fast_tiling(B, T, D, vec_of(x_dt), kFwdNW, 16, 64, 4096, tune().fwd_rows);
+  const FastShape sh = shape_of<FwdCfg>(x_dt);
+  return fast_tiling(B, T, D, sh.cpl, sh.nw, 16, 64, 4096, tune().fwd_rows);
 }
 
 Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
-  return fast_tiling(B, T, D, vec_of(x_dt), kBwdNW, 32, 64, 2048, tune().bwd_rows);
+  const FastShape sh = shape_of<BwdCfg>(x_dt);
+  return fast_tiling(B, T, D, sh.cpl, sh.nw, 32, 64, 4096, tune().bwd_rows);
 }
 
 Tiling generic_tiling(int64_t T) {
@@ -132,12 +146,25 @@ int check_common(const void* x, int64_t s_xb, int64_t s_xt, int x_dt, const void
   return CCV1D_OK;
 }
 
-// The vectorised kernels need 16-byte rows: dim a multiple of the vector, aligned bases and strides.
-bool fast_ok(int x_dt, int64_t D, int64_t W, const void* x, int64_t s_xb, int64_t s_xt) {
-  if (W > kMaxFastW || x_dt == CCV1D_F64) return false;
-  const int v = vec_of(x_dt);
-  return D % v == 0 && aligned16(x) && s_xb % v == 0 && s_xt % v == 0;
+// The vectorised kernels read and write rows of `cpl` channels per lane: dim a multiple of cpl, the
+// base and the strides aligned to the access width, and every byte offset inside one batch slab
+// below 2^32 (they address rows through 32-bit buffer offsets).
+bool rows_ok(int x_dt, int cpl, int64_t T, int64_t D, const void* p, int64_t s_b, int64_t s_t) {
+  const int64_t esz = esize(x_dt);
+  if (D % cpl || s_b % cpl || s_t % cpl) return false;
+  if (reinterpret_cast<uintptr_t>(p) % (uintptr_t)(cpl * esz)) return false;
+  return ((T - 1) * s_t + D) * esz < (int64_t(1) << 32);
 }
+
+bool aligned_to(const void* p, int64_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)bytes) == 0;
+}
+
+uint32_t slab_bytes(int x_dt, int64_t T, int64_t D, int64_t s_t) {
+  return (uint32_t)(((T - 1) * s_t + D) * esize(x_dt));
+}
+
+bool fast_dtype(int x_dt, int64_t W) { return W <= kMaxFastW && x_dt != CCV1D_F64; }
 
 }  // namespace
 
@@ -161,8 +188,11 @@ int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
     return fail(CCV1D_ERR_INVALID, "cannot return final states if seq_idx is given");
   if (B * T * D > 0 && !out) return fail(CCV1D_ERR_INVALID, "out is null");
   if (B * D == 0) return CCV1D_OK;
-  const bool fast = T > 0 && fast_ok(x_dtype, D, W, x, x_stride_b, x_stride_t) && aligned16(out) &&
-                    (!final_states || aligned16(final_states));
+  const int fcpl = shape_of<FwdCfg>(x_dtype).cpl;
+  const bool fast = T > 0 && fast_dtype(x_dtype, W) &&
+                    rows_ok(x_dtype, fcpl, T, D, x, x_stride_b, x_stride_t) &&
+                    rows_ok(x_dtype, fcpl, T, D, out, T * D, D) &&
+                    (!final_states || aligned_to(final_states, fcpl * esize(x_dtype)));
   Tiling tl{};
   if (T > 0) {
     if (fast) {
@@ -208,6 +238,10 @@ int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   p.has_init = initial_states != nullptr;
   p.has_final = final_states != nullptr;
   p.silu = silu != 0;
+  if (fast) {
+    p.x_bytes = slab_bytes(x_dtype, T, D, x_stride_t);
+    p.o_bytes = slab_bytes(x_dtype, T, D, D);
+  }
 
   p.tl = tl;
   hipError_t e;
@@ -266,9 +300,13 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
     return fail(CCV1D_ERR_INVALID, "cannot take final-state gradients if seq_idx is given");
   if (D == 0) return CCV1D_OK;
   const bool empty = B == 0 || T == 0;
-  const bool fast = !empty && fast_ok(x_dtype, D, W, x, x_stride_b, x_stride_t) &&
-                    fast_ok(x_dtype, D, W, dout, dout_stride_b, dout_stride_t) && aligned16(dx) &&
-                    (!dfinal_states || aligned16(dfinal_states)) && aligned16(workspace);
+  const int bcpl = shape_of<BwdCfg>(x_dtype).cpl;
+  const bool fast = !empty && fast_dtype(x_dtype, W) &&
+                    rows_ok(x_dtype, bcpl, T, D, x, x_stride_b, x_stride_t) &&
+                    rows_ok(x_dtype, bcpl, T, D, dout, dout_stride_b, dout_stride_t) &&
+                    rows_ok(x_dtype, bcpl, T, D, dx, T * D, D) &&
+                    (!dfinal_states || aligned_to(dfinal_states, bcpl * esize(x_dtype))) &&
+                    aligned_to(workspace, 16);
   Tiling tl{};
   int64_t rows = 0;
   if (!empty) {
@@ -329,6 +367,11 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   p.has_dfinal = dfinal_states != nullptr;
   p.need_dinit = dinitial_states != nullptr;
   p.silu = silu != 0;
+  if (fast) {
+    p.x_bytes = slab_bytes(x_dtype, T, D, x_stride_t);
+    p.y_bytes = slab_bytes(x_dtype, T, D, dout_stride_t);
+    p.o_bytes = slab_bytes(x_dtype, T, D, D);
+  }
 
   p.tl = tl;
   hipError_t e;

@@ -36,6 +36,7 @@ struct FwdParams {
   int32_t B, T, D, W;
   int32_t w_dt, b_dt, i_dt;
   int32_t has_bias, has_init, has_final, silu;
+  uint32_t x_bytes, o_bytes;  // per-batch byte extents of x and out (vectorised kernels)
   Tiling tl;
 };
 
@@ -55,6 +56,7 @@ struct BwdParams {
   int32_t B, T, D, W;
   int32_t w_dt, b_dt, i_dt;
   int32_t has_bias, has_init, has_dfinal, need_dinit, silu;
+  uint32_t x_bytes, y_bytes, o_bytes;  // per-batch byte extents of x, dout and dx
   Tiling tl;
 };
 
@@ -90,77 +92,167 @@ __device__ __forceinline__ void st_any(void* p, int64_t i, int dt, float v) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// 16-byte channel vectors of the x dtype. One lane moves VEC consecutive channels of one row with a
-// single 128-bit load or store; a wave therefore covers 64 * VEC channels (1 KiB) per instruction.
+// Channel vectors of the x dtype. One lane moves CPL consecutive channels of one row with a single
+// 8- or 16-byte load or store, so a wave covers 64 * CPL channels (512 B or 1 KiB) per instruction.
 // ---------------------------------------------------------------------------------------------
 
 typedef float f2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf2v __attribute__((ext_vector_type(2)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <typename TX> struct Vec16;
+template <int BYTES> struct RawOf;
+template <> struct RawOf<8> { using type = u32x2; };
+template <> struct RawOf<16> { using type = u32x4; };
 
-template <> struct Vec16<__bf16> {
-  static constexpr int VEC = 8;
-  __device__ static __forceinline__ void unpack(const uint4 v, float (&f)[8]) {
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+template <typename TX, int CPL>
+struct VecIO {
+  static constexpr int BYTES = CPL * (int)sizeof(TX);
+  static constexpr int WORDS = BYTES / 4;
+  using raw = typename RawOf<BYTES>::type;
+
+  __device__ static __forceinline__ raw ld(const TX* p) { return *reinterpret_cast<const raw*>(p); }
+  __device__ static __forceinline__ void st(TX* p, raw v) { *reinterpret_cast<raw*>(p) = v; }
+  // Non-temporal store: streamed output that no later work in the kernel reads.
+  __device__ static __forceinline__ void st_nt(TX* p, raw v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<raw*>(p));
+  }
+
+  __device__ static __forceinline__ void unpack(const raw v, float (&f)[CPL]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f[2 * j] = __uint_as_float(u[j] << 16);
-      f[2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+    for (int j = 0; j < WORDS; ++j) {
+      const uint32_t u = v[j];
+      if constexpr (sizeof(TX) == 4) {
+        f[j] = __uint_as_float(u);
+      } else if constexpr (__is_same(TX, __bf16)) {
+        f[2 * j] = __uint_as_float(u << 16);
+        f[2 * j + 1] = __uint_as_float(u & 0xffff0000u);
+      } else {
+        const f2v q = __builtin_convertvector(__builtin_bit_cast(h2v, u), f2v);
+        f[2 * j] = q.x;
+        f[2 * j + 1] = q.y;
+      }
     }
   }
-  __device__ static __forceinline__ uint4 pack(const float (&f)[8]) {
-    uint32_t u[4];
+
+  // Round-to-nearest-even; one v_cvt_pk_{bf16,f16}_f32 per channel pair.
+  __device__ static __forceinline__ raw pack(const float (&f)[CPL]) {
+    raw v;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // Round-to-nearest-even, one v_cvt_pk_bf16_f32 per channel pair.
-      u[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){f[2 * j], f[2 * j + 1]}, bf2v));
+    for (int j = 0; j < WORDS; ++j) {
+      if constexpr (sizeof(TX) == 4) {
+        v[j] = __float_as_uint(f[j]);
+      } else if constexpr (__is_same(TX, __bf16)) {
+        v[j] = __builtin_bit_cast(uint32_t,
+                                  __builtin_convertvector((f2v){f[2 * j], f[2 * j + 1]}, bf2v));
+      } else {
+        v[j] = __builtin_bit_cast(uint32_t,
+                                  __builtin_convertvector((f2v){f[2 * j], f[2 * j + 1]}, h2v));
+      }
     }
-    return make_uint4(u[0], u[1], u[2], u[3]);
+    return v;
   }
 };
 
-template <> struct Vec16<_Float16> {
-  static constexpr int VEC = 8;
-  __device__ static __forceinline__ void unpack(const uint4 v, float (&f)[8]) {
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f2v p = __builtin_convertvector(__builtin_bit_cast(h2v, u[j]), f2v);
-      f[2 * j] = p.x;
-      f[2 * j + 1] = p.y;
-    }
+// Rows of one batch slab of a channels-last tensor. Loads go through a buffer resource: the row
+// offset is a uniform (scalar) byte offset and the lane's channel offset a 32-bit vector offset, so a
+// row load costs no vector address arithmetic. The host guarantees every byte offset used here is
+// below 2^32 and below `extent`, the resource's size.
+//
+// Stores of 8 bytes use the same resource. 16-byte stores use a global store instead: after a
+// buffer_store_dwordx4 whose offset is in an SGPR the compiler does not keep the data VGPRs intact
+// for the wait state a store of more than 8 bytes needs before a VALU may overwrite them, and on
+// gfx950 such stores were measured to write values of the following instructions. The compiler does
+// enforce that wait state after global stores.
+template <typename TX, int CPL>
+struct RowBuf {
+  using IO = VecIO<TX, CPL>;
+  using raw = typename IO::raw;
+  __amdgpu_buffer_rsrc_t rs;
+  const TX* base;      // row 0, channel 0 of the slab
+  uint32_t lane_off;   // byte offset of this lane's first channel
+  uint32_t row_bytes;  // time stride in bytes
+
+  __device__ __forceinline__ RowBuf(const TX* slab, uint32_t extent, int c0, int stride_t) {
+    rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<TX*>(slab), 0, (int)extent, 0x00020000);
+    base = slab;
+    lane_off = (uint32_t)c0 * (uint32_t)sizeof(TX);
+    row_bytes = (uint32_t)stride_t * (uint32_t)sizeof(TX);
   }
-  __device__ static __forceinline__ uint4 pack(const float (&f)[8]) {
-    uint32_t u[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){f[2 * j], f[2 * j + 1]}, h2v));
+  __device__ __forceinline__ raw ld(int row) const {
+    if constexpr (IO::BYTES == 16)
+      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, (uint32_t)row * row_bytes, 0));
+    else
+      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b64(rs, lane_off, (uint32_t)row * row_bytes, 0));
+  }
+  // NT: non-temporal store (a streamed output that no later work of the kernel reads).
+  template <bool NT>
+  __device__ __forceinline__ void st(int row, raw v) const {
+    if constexpr (IO::BYTES == 16) {
+      TX* p = reinterpret_cast<TX*>(const_cast<char*>(reinterpret_cast<const char*>(base)) +
+                                    (uint64_t)((uint32_t)row * row_bytes + lane_off));
+      if (NT) IO::st_nt(p, v);
+      else IO::st(p, v);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), rs, lane_off,
+                                            (uint32_t)row * row_bytes, NT ? 2 : 0);
     }
-    return make_uint4(u[0], u[1], u[2], u[3]);
   }
 };
 
-template <> struct Vec16<float> {
-  static constexpr int VEC = 4;
-  __device__ static __forceinline__ void unpack(const uint4 v, float (&f)[4]) {
-    f[0] = __uint_as_float(v.x);
-    f[1] = __uint_as_float(v.y);
-    f[2] = __uint_as_float(v.z);
-    f[3] = __uint_as_float(v.w);
+// N consecutive elements of a side tensor whose dtype is a runtime code, converted to fp32. The
+// dtype switch is taken once for the whole vector so the N loads issue together.
+template <int N>
+__device__ __forceinline__ void ld_vec_any(const void* p, int64_t off, int dt, float (&f)[N]) {
+  switch (dt) {
+    case DT_F32: {
+      const float* q = static_cast<const float*>(p) + off;
+#pragma unroll
+      for (int i = 0; i < N; ++i) f[i] = q[i];
+    } break;
+    case DT_F16: {
+      const _Float16* q = static_cast<const _Float16*>(p) + off;
+#pragma unroll
+      for (int i = 0; i < N; ++i) f[i] = static_cast<float>(q[i]);
+    } break;
+    case DT_BF16: {
+      const __bf16* q = static_cast<const __bf16*>(p) + off;
+#pragma unroll
+      for (int i = 0; i < N; ++i) f[i] = static_cast<float>(q[i]);
+    } break;
+    default: {
+      const double* q = static_cast<const double*>(p) + off;
+#pragma unroll
+      for (int i = 0; i < N; ++i) f[i] = static_cast<float>(q[i]);
+    } break;
   }
-  __device__ static __forceinline__ uint4 pack(const float (&f)[4]) {
-    return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
-                      __float_as_uint(f[3]));
-  }
-};
-
-template <typename TX> __device__ __forceinline__ uint4 ld16(const TX* p) {
-  return *reinterpret_cast<const uint4*>(p);
 }
-template <typename TX> __device__ __forceinline__ void st16(TX* p, uint4 v) {
-  *reinterpret_cast<uint4*>(p) = v;
+
+template <int N>
+__device__ __forceinline__ void st_vec_any(void* p, int64_t off, int dt, const float (&f)[N]) {
+  switch (dt) {
+    case DT_F32: {
+      float* q = static_cast<float*>(p) + off;
+#pragma unroll
+      for (int i = 0; i < N; ++i) q[i] = f[i];
+    } break;
+    case DT_F16: {
+      _Float16* q = static_cast<_Float16*>(p) + off;
+#pragma unroll
+      for (int i = 0; i < N; ++i) q[i] = static_cast<_Float16>(f[i]);
+    } break;
+    case DT_BF16: {
+      __bf16* q = static_cast<__bf16*>(p) + off;
+#pragma unroll
+      for (int i = 0; i < N; ++i) q[i] = static_cast<__bf16>(f[i]);
+    } break;
+    default: {
+      double* q = static_cast<double*>(p) + off;
+#pragma unroll
+      for (int i = 0; i < N; ++i) q[i] = static_cast<double>(f[i]);
+    } break;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -1,94 +1,77 @@
-// Vectorised forward and backward kernels for compile-time widths (2..8), channels-last x whose
-// rows are 16-byte aligned.
+// Vectorised forward and backward kernels for compile-time widths (2..8) and channels-last x whose
+// rows are 8- or 16-byte aligned.
 //
-// Work decomposition (both passes): a lane owns VEC = 16 / sizeof(x) consecutive channels, a wave
-// owns 64 such channel vectors (1 KiB of one row) over a tile of L consecutive rows, and a workgroup
-// holds NW waves on consecutive tiles of the same channel range. Each wave walks forward in time and
-// keeps the previous width - 1 rows in registers, so every row of x is loaded once per tile plus a
-// (width - 1)-row halo that the neighbouring tile of the same workgroup (same CU) or of the same XCD
-// (see xcd_remap) has just loaded.
+// Work decomposition (both passes): a lane owns CPL consecutive channels, a wave owns 64 such
+// channel vectors over a tile of L consecutive rows, and a workgroup holds NW waves on consecutive
+// tiles of the same channel range. Each wave walks forward in time with the previous width - 1 rows
+// in registers, so a row of x is loaded once per tile plus a (width - 1)-row halo that the
+// neighbouring tile of the same workgroup (same CU) or of the same XCD (xcd_remap) has just read.
+// Rows are processed in batches of R: the loads of batch k + 1 are issued before batch k is
+// computed, so every wave keeps up to 2R rows of reads in flight while its ALUs work.
 #pragma once
 
 #include "ccv1d_device.h"
 
 namespace ccv1d {
 
-// Row `row` (>= -P) of concat(initial_states, x) for this lane's VEC channels, in fp32
-// (causal_conv1d.py:28-41). xb points at x[b, 0, c0], initb at initial_states[b, 0, c0].
-template <typename TX, int VEC, int P>
-__device__ __forceinline__ void load_row(const TX* xb, int s_xt, const void* initb, int i_dt,
-                                         bool has_init, int D, int row, float (&f)[VEC]) {
-  if (row >= 0) {
-    Vec16<TX>::unpack(ld16(xb + row * s_xt), f);
-  } else if (has_init) {
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) f[i] = ld_any(initb, (int64_t)(row + P) * D + i, i_dt);
-  } else {
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) f[i] = 0.0f;
-  }
-}
-
-// Weights (D, W) and bias (D) for channels c0 .. c0 + VEC - 1, in fp32.
-template <int W, int VEC>
+// Weights (D, W) and bias (D) for channels c0 .. c0 + CPL - 1, in fp32.
+template <int W, int CPL>
 __device__ __forceinline__ void load_taps(const void* w, int w_dt, const void* bias, int b_dt,
-                                          bool has_bias, int c0, float (&wv)[W][VEC],
-                                          float (&bv)[VEC]) {
-  if (w_dt == DT_F32) {
-    const float* wp = static_cast<const float*>(w) + (int64_t)c0 * W;
+                                          bool has_bias, int c0, float (&wv)[W][CPL],
+                                          float (&bv)[CPL]) {
+  float flat[W * CPL];
+  ld_vec_any<W * CPL>(w, (int64_t)c0 * W, w_dt, flat);
 #pragma unroll
-    for (int i = 0; i < VEC; ++i)
+  for (int i = 0; i < CPL; ++i)
 #pragma unroll
-      for (int k = 0; k < W; ++k) wv[k][i] = wp[i * W + k];
+    for (int k = 0; k < W; ++k) wv[k][i] = flat[i * W + k];
+  if (has_bias) {
+    ld_vec_any<CPL>(bias, c0, b_dt, bv);
   } else {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i)
-#pragma unroll
-      for (int k = 0; k < W; ++k) wv[k][i] = ld_any(w, (int64_t)(c0 + i) * W + k, w_dt);
+    for (int i = 0; i < CPL; ++i) bv[i] = 0.0f;
   }
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) bv[i] = has_bias ? ld_any(bias, c0 + i, b_dt) : 0.0f;
 }
 
 // Pre-activation of one row (causal_conv1d.py:129-138), in the reference's order:
 //   z = w[P] * x[t]; z = fma(w[k], x[t-P+k], z) for k = 0..P-1 (masked by sequence equality);
 //   z += bias; with ZERO_PAD, z = 0 on padding rows (sequence id < 0).
 // xw holds rows t-P .. t-1, sw their sequence ids; xc is row t and st its sequence id.
-template <int W, int VEC, bool SEQ, bool ZERO_PAD>
-__device__ __forceinline__ void conv_row(const float (&wv)[W][VEC], const float (&bv)[VEC],
-                                         bool has_bias, const float (&xw)[W - 1][VEC],
-                                         const int32_t (&sw)[W - 1], const float (&xc)[VEC],
-                                         int32_t st, float (&z)[VEC]) {
+template <int W, int CPL, bool SEQ, bool ZERO_PAD>
+__device__ __forceinline__ void conv_row(const float (&wv)[W][CPL], const float (&bv)[CPL],
+                                         bool has_bias, const float (&xw)[W - 1][CPL],
+                                         const int32_t (&sw)[W - 1], const float (&xc)[CPL],
+                                         int32_t st, float (&z)[CPL]) {
   constexpr int P = W - 1;
 #pragma unroll
-  for (int i = 0; i < VEC; ++i) z[i] = wv[P][i] * xc[i];
+  for (int i = 0; i < CPL; ++i) z[i] = wv[P][i] * xc[i];
 #pragma unroll
   for (int k = 0; k < P; ++k) {
     const bool m = !SEQ || sw[k] == st;
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
+    for (int i = 0; i < CPL; ++i) {
       const float f = fmaf(wv[k][i], xw[k][i], z[i]);
       z[i] = m ? f : z[i];
     }
   }
   if (has_bias) {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) z[i] += bv[i];
+    for (int i = 0; i < CPL; ++i) z[i] += bv[i];
   }
   if (SEQ && ZERO_PAD && st < 0) {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) z[i] = 0.0f;
+    for (int i = 0; i < CPL; ++i) z[i] = 0.0f;
   }
 }
 
-template <int P, int VEC>
-__device__ __forceinline__ void shift_in(float (&win)[P][VEC], const float (&v)[VEC]) {
+template <int P, int CPL>
+__device__ __forceinline__ void shift_in(float (&win)[P][CPL], const float (&v)[CPL]) {
 #pragma unroll
   for (int k = 0; k + 1 < P; ++k)
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) win[k][i] = win[k + 1][i];
+    for (int i = 0; i < CPL; ++i) win[k][i] = win[k + 1][i];
 #pragma unroll
-  for (int i = 0; i < VEC; ++i) win[P - 1][i] = v[i];
+  for (int i = 0; i < CPL; ++i) win[P - 1][i] = v[i];
 }
 
 template <int P>
@@ -98,101 +81,142 @@ __device__ __forceinline__ void shift_in(int32_t (&win)[P], int32_t v) {
   win[P - 1] = v;
 }
 
+// Workgroup -> (batch row, wave column, workgroup along time), with neighbouring time tiles kept
+// on one XCD.
+struct TileCoord {
+  int b, gw, tb;
+  __device__ __forceinline__ TileCoord(const Tiling& tl) {
+    const int blk = xcd_remap(blockIdx.x, tl.nBlk);
+    tb = blk % tl.nTB;
+    const int rest = blk / tl.nTB;
+    gw = rest % tl.nGW;
+    b = rest / tl.nGW;
+  }
+};
+
 // =============================================================================================
 // Forward: out = act(conv(x)) and final_states (causal_conv1d.py:44-164).
 // =============================================================================================
 
-template <typename TX, int W, bool SILU, bool SEQ>
+template <typename TX, int W, bool SILU, bool SEQ, int CPL>
 struct FwdLane {
-  static constexpr int VEC = Vec16<TX>::VEC;
+  using IO = VecIO<TX, CPL>;
+  using raw = typename IO::raw;
   static constexpr int P = W - 1;
-  float wv[W][VEC];
-  float bv[VEC];
-  float xw[P][VEC];   // rows t-P .. t-1
-  int32_t sw[P];      // their sequence ids
+  float wv[W][CPL];
+  float bv[CPL];
+  float xw[P][CPL];  // rows t-P .. t-1
+  int32_t sw[P];     // their sequence ids
+  bool has_bias;
 
-  // One output row t from its input row xc (already unpacked) and sequence id st.
-  __device__ __forceinline__ void step(bool has_bias, const float (&xc)[VEC], int32_t st, TX* orow) {
-    float z[VEC];
-    conv_row<W, VEC, SEQ, true>(wv, bv, has_bias, xw, sw, xc, st, z);
+  // Output row t from its raw input row and sequence id.
+  __device__ __forceinline__ raw row(const raw xr, int32_t st) {
+    float xc[CPL], z[CPL];
+    IO::unpack(xr, xc);
+    conv_row<W, CPL, SEQ, true>(wv, bv, has_bias, xw, sw, xc, st, z);
     if (SILU) {
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) z[i] = z[i] * sigmoid_f(z[i]);
+      for (int i = 0; i < CPL; ++i) z[i] = z[i] * sigmoid_f(z[i]);
     }
-    st16(orow, Vec16<TX>::pack(z));
     shift_in(xw, xc);
     if (SEQ) shift_in(sw, st);
+    return IO::pack(z);
   }
 };
 
-template <typename TX, int W, bool SILU, bool SEQ, int NW, int R>
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, bool NTS>
 __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
-  using V = Vec16<TX>;
-  constexpr int VEC = V::VEC;
+  using IO = VecIO<TX, CPL>;
+  using raw = typename IO::raw;
   constexpr int P = W - 1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int blk = xcd_remap(blockIdx.x, p.tl.nBlk);
-  const int tb = blk % p.tl.nTB;
-  const int rest = blk / p.tl.nTB;
-  const int gw = rest % p.tl.nGW;
-  const int b = rest / p.tl.nGW;
-  const int tile = tb * NW + wave;
+  const TileCoord tc(p.tl);
+  const int tile = tc.tb * NW + wave;
   if (tile >= p.tl.nT) return;
-  const int grp = gw * 64 + lane;
-  if (grp >= p.D / VEC) return;
-  const int c0 = grp * VEC;
-  const int T = p.T, D = p.D, s_xt = p.s_xt;
+  const int grp = tc.gw * 64 + lane;
+  if (grp >= p.D / CPL) return;
+  const int c0 = grp * CPL;
+  const int T = p.T, D = p.D;
   const int t0 = tile * p.tl.L;
   const int t1 = min(t0 + p.tl.L, T);
-  const bool has_bias = p.has_bias, has_init = p.has_init;
+  const bool has_init = p.has_init;
 
-  const TX* xb = static_cast<const TX*>(p.x) + (int64_t)b * p.s_xb + c0;
-  TX* ob = static_cast<TX*>(p.out) + (int64_t)b * T * D + c0;
-  const int32_t* sb = SEQ ? p.seq + (int64_t)b * T : nullptr;
-  const void* initb = nullptr;
-  if (has_init) initb = static_cast<const char*>(p.init) +
-                        ((int64_t)b * P * D + c0) * (p.i_dt == DT_F64 ? 8 : p.i_dt == DT_F32 ? 4 : 2);
+  const RowBuf<TX, CPL> X(static_cast<const TX*>(p.x) + (int64_t)tc.b * p.s_xb, p.x_bytes, c0, p.s_xt);
+  const RowBuf<TX, CPL> O(static_cast<const TX*>(p.out) + (int64_t)tc.b * T * D, p.o_bytes, c0, D);
+  const int32_t* __restrict__ sb = SEQ ? p.seq + (int64_t)tc.b * T : nullptr;
+  const int64_t init_off = (int64_t)tc.b * P * D + c0;
 
-  FwdLane<TX, W, SILU, SEQ> s;
-  load_taps<W, VEC>(p.w, p.w_dt, p.bias, p.b_dt, has_bias, c0, s.wv, s.bv);
+  // Halo rows, the first batch and the taps are requested together.
+  const bool halo_in_x = t0 >= P;
+  raw hr[P];
+  if (halo_in_x) {
+#pragma unroll
+    for (int k = 0; k < P; ++k) hr[k] = X.ld(t0 - P + k);
+  }
+  raw A[R], B[R];
+  int32_t sA[R], sB[R];
+  auto load = [&](raw (&buf)[R], int32_t (&sq)[R], int t) {
+    // Rows past the tile end are clamped to its last row: a duplicate read keeps the number of
+    // loads in flight independent of the tile length, so the compiler's wait counts stay exact.
+#pragma unroll
+    for (int r = 0; r < R; ++r) buf[r] = X.ld(min(t + r, t1 - 1));
+#pragma unroll
+    for (int r = 0; r < R; ++r) sq[r] = SEQ ? sb[min(t + r, t1 - 1)] : 0;
+  };
+  load(A, sA, t0);
+
+  FwdLane<TX, W, SILU, SEQ, CPL> s;
+  s.has_bias = p.has_bias;
+  load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
 #pragma unroll
   for (int k = 0; k < P; ++k) {
-    const int row = t0 - P + k;
-    load_row<TX, VEC, P>(xb, s_xt, initb, p.i_dt, has_init, D, row, s.xw[k]);
-    s.sw[k] = SEQ ? seq_at(sb, row, T, has_init) : 0;
+    if (halo_in_x) IO::unpack(hr[k], s.xw[k]);
+    else {
+      const int row = t0 - P + k;
+      if (row >= 0) IO::unpack(X.ld(row), s.xw[k]);
+      else if (has_init) ld_vec_any<CPL>(p.init, init_off + (int64_t)(row + P) * D, p.i_dt, s.xw[k]);
+      else {
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) s.xw[k][i] = 0.0f;
+      }
+    }
+    s.sw[k] = SEQ ? seq_at(sb, t0 - P + k, T, has_init) : 0;
   }
 
+  auto compute = [&](const raw (&buf)[R], const int32_t (&sq)[R], int t) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) O.template st<NTS>(t + r, s.row(buf[r], sq[r]));
+  };
+
+  // Ping-pong over two register batches: batch k + 1 is in flight while batch k is computed.
   int t = t0;
-  // Full batches: the R row loads are issued together, ahead of the first use.
-  for (; t + R <= t1; t += R) {
-    uint4 raw[R];
-    int32_t sr[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) raw[r] = ld16(xb + (t + r) * s_xt);
-#pragma unroll
-    for (int r = 0; r < R; ++r) sr[r] = SEQ ? sb[t + r] : 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float xc[VEC];
-      V::unpack(raw[r], xc);
-      s.step(has_bias, xc, sr[r], ob + (t + r) * D);
-    }
+  for (; t + 2 * R <= t1; t += 2 * R) {
+    load(B, sB, t + R);
+    compute(A, sA, t);
+    load(A, sA, t + 2 * R);
+    compute(B, sB, t + R);
   }
-  for (; t < t1; ++t) {
-    float xc[VEC];
-    V::unpack(ld16(xb + t * s_xt), xc);
-    s.step(has_bias, xc, SEQ ? sb[t] : 0, ob + t * D);
+  if (t + R <= t1) {
+    compute(A, sA, t);
+    t += R;
   }
+  for (; t < t1; ++t) O.template st<NTS>(t, s.row(X.ld(t), SEQ ? sb[t] : 0));
 
   // final_states = rows T-P .. T-1 of concat(initial_states, x) (causal_conv1d.py:153-164).
   if (p.has_final && t1 == T) {
-    TX* fb = static_cast<TX*>(p.fin) + (int64_t)b * P * D + c0;
+    TX* fb = static_cast<TX*>(p.fin) + init_off;
 #pragma unroll
     for (int q = 0; q < P; ++q) {
-      float f[VEC];
-      load_row<TX, VEC, P>(xb, s_xt, initb, p.i_dt, has_init, D, T - P + q, f);
-      st16(fb + q * D, V::pack(f));
+      const int row = T - P + q;
+      float f[CPL];
+      if (row >= 0) IO::unpack(X.ld(row), f);
+      else if (has_init) ld_vec_any<CPL>(p.init, init_off + (int64_t)(row + P) * D, p.i_dt, f);
+      else {
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) f[i] = 0.0f;
+      }
+      IO::st(fb + q * D, IO::pack(f));
     }
   }
 }
@@ -205,214 +229,272 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
 //   dx[t-P] = w[P] g[t-P] + sum_{j=1..P} m_j w[P-j] g[t-P+j]     (+ dfinal where it applies)
 // whose last term needs the current row. The tile runs P rows past its end (right halo) so its
 // last P dx rows are complete; those halo rows add nothing to dweight. Tile 0 also emits rows
-// -P..-1 (the initial-state gradient). dweight/dbias sums are combined across the workgroup's
-// waves in LDS in wave order, and written as one fp32 partial row per workgroup.
+// -P..-1 (the initial-state gradient). The first P rows of a tile (where those initial-state rows
+// and the rows of the previous tile come out) and the rows past T (where dfinal enters) are handled
+// outside the pipelined loop, whose every step therefore ends in one plain dx store.
+// dweight/dbias sums are combined across the workgroup's waves in LDS in wave order and written as
+// one fp32 partial row per workgroup.
 // =============================================================================================
 
-template <typename TX, int W, bool SILU, bool SEQ>
+template <typename TX, int W, bool SILU, bool SEQ, int CPL>
 struct BwdLane {
-  static constexpr int VEC = Vec16<TX>::VEC;
+  using IO = VecIO<TX, CPL>;
+  using raw = typename IO::raw;
   static constexpr int P = W - 1;
-  float wv[W][VEC];
-  float bv[VEC];
-  float xw[P][VEC];   // x rows t-P .. t-1
-  float gw[P][VEC];   // g rows t-P .. t-1
+  float wv[W][CPL];
+  float bv[CPL];
+  float xw[P][CPL];   // x rows t-P .. t-1
+  float gw[P][CPL];   // g rows t-P .. t-1
   int32_t sw[P];      // sequence ids of rows t-P .. t-1
-  float dw[W][VEC];
-  float db[VEC];
+  float dw[W][CPL];
+  float db[CPL];
+  bool has_bias;
+  int own_end;
 
-  // dx of row `row` = t - P given g of row t (gt) and its sequence id (st), then the dfinal term.
-  __device__ __forceinline__ void dx_row(const float (&gt)[VEC], int32_t st, float (&dx)[VEC]) {
+  // dx of row t - P, given g of row t (gt) and its sequence id (st).
+  __device__ __forceinline__ void dx_row(const float (&gt)[CPL], int32_t st, bool with_last,
+                                         float (&dx)[CPL]) const {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) dx[i] = wv[P][i] * gw[0][i];
+    for (int i = 0; i < CPL; ++i) dx[i] = wv[P][i] * gw[0][i];
 #pragma unroll
     for (int j = 1; j < P; ++j) {
       const bool m = !SEQ || sw[j] == sw[0];
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) {
+      for (int i = 0; i < CPL; ++i) {
         const float f = fmaf(wv[P - j][i], gw[j][i], dx[i]);
         dx[i] = m ? f : dx[i];
       }
     }
-    const bool m = !SEQ || st == sw[0];
+    if (with_last) {
+      const bool m = !SEQ || st == sw[0];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      const float f = fmaf(wv[0][i], gt[i], dx[i]);
-      dx[i] = m ? f : dx[i];
+      for (int i = 0; i < CPL; ++i) {
+        const float f = fmaf(wv[0][i], gt[i], dx[i]);
+        dx[i] = m ? f : dx[i];
+      }
     }
+  }
+
+  // One row t = tt: g, dweight/dbias (own rows), and dx of row tt - P in `dx`; shifts the windows.
+  __device__ __forceinline__ void step(int tt, const raw xr, const raw yr, int32_t st,
+                                       float (&dx)[CPL]) {
+    float xc[CPL], g[CPL];
+    IO::unpack(xr, xc);
+    IO::unpack(yr, g);
+    if (SILU) {
+      float z[CPL];
+      conv_row<W, CPL, SEQ, false>(wv, bv, has_bias, xw, sw, xc, st, z);
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) g[i] = dsilu_times(g[i], z[i]);
+    }
+    if (SEQ && st < 0) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) g[i] = 0.0f;
+    }
+    if (tt < own_end) {
+#pragma unroll
+      for (int k = 0; k < P; ++k) {
+        const bool m = !SEQ || sw[k] == st;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          const float f = fmaf(g[i], xw[k][i], dw[k][i]);
+          dw[k][i] = m ? f : dw[k][i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        dw[P][i] = fmaf(g[i], xc[i], dw[P][i]);
+        db[i] += g[i];
+      }
+    }
+    dx_row(g, st, true, dx);
+    shift_in(xw, xc);
+    shift_in(gw, g);
+    if (SEQ) shift_in(sw, st);
   }
 };
 
-template <typename TX, int W, bool SILU, bool SEQ, int NW, int R>
+// Barrier for data exchanged through LDS only: waits for this wave's LDS operations, not for its
+// global loads, so prefetches stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, bool NTS>
 __global__ __launch_bounds__(NW * 64) void bwd_fast_kernel(const BwdParams p) {
-  using V = Vec16<TX>;
-  constexpr int VEC = V::VEC;
+  using IO = VecIO<TX, CPL>;
+  using raw = typename IO::raw;
   constexpr int P = W - 1;
-  __shared__ float red[(NW > 1 ? NW - 1 : 1) * (W + 1) * 64 * VEC];
+  constexpr int COLS = 64 * CPL;
+  // LDS: first the g values of every wave's first P rows (the right halo of the wave before it),
+  // later the dweight/dbias sums of waves 1..NW-1.
+  constexpr int HALO_FLOATS = NW * P * COLS;
+  constexpr int RED_FLOATS = (NW > 1 ? NW - 1 : 1) * (W + 1) * COLS;
+  __shared__ float lds[HALO_FLOATS > RED_FLOATS ? HALO_FLOATS : RED_FLOATS];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int blk = xcd_remap(blockIdx.x, p.tl.nBlk);
-  const int tb = blk % p.tl.nTB;
-  const int rest = blk / p.tl.nTB;
-  const int gwc = rest % p.tl.nGW;
-  const int b = rest / p.tl.nGW;
-  const int tile = tb * NW + wave;
-  const int G = p.D / VEC;
-  const int grp = gwc * 64 + lane;
-  const int c0 = grp * VEC;
+  const TileCoord tc(p.tl);
+  const int tile = tc.tb * NW + wave;
+  const int G = p.D / CPL;
+  const int grp = tc.gw * 64 + lane;
+  const int c0 = grp * CPL;
   const int T = p.T, D = p.D;
-  const bool has_bias = p.has_bias;
+  const bool active = tile < p.tl.nT && grp < G;
+  const bool has_init = p.has_init;
+  const int t0 = tile * p.tl.L;
+  const int own_end = min(t0 + p.tl.L, T);
+  // The next tile's first P rows of g come from its wave through LDS when it is in this workgroup;
+  // otherwise this wave computes them itself (the right halo).
+  const bool succ_here = wave < NW - 1 && tile + 1 < p.tl.nT;
+  const int t_end = succ_here ? own_end : min(own_end + P, T);
+  const int t_main = min(t0 + P, t_end);
+  const int emit_lo = (tile == 0 && p.need_dinit) ? -P : t0;
+  const int64_t state_off = (int64_t)tc.b * P * D + c0;
+  const int32_t* __restrict__ sb = SEQ ? p.seq + (int64_t)tc.b * T : nullptr;
+  const TX* dfb = p.has_dfinal ? static_cast<const TX*>(p.dfin) + state_off : nullptr;
+  const RowBuf<TX, CPL> X(static_cast<const TX*>(p.x) + (int64_t)tc.b * p.s_xb, p.x_bytes, c0, p.s_xt);
+  const RowBuf<TX, CPL> Y(static_cast<const TX*>(p.dy) + (int64_t)tc.b * p.s_yb, p.y_bytes, c0, p.s_yt);
+  const RowBuf<TX, CPL> DX(static_cast<const TX*>(p.dx) + (int64_t)tc.b * T * D, p.o_bytes, c0, D);
 
-  BwdLane<TX, W, SILU, SEQ> s;
+  BwdLane<TX, W, SILU, SEQ, CPL> s;
+  s.has_bias = p.has_bias;
+  s.own_end = own_end;
 #pragma unroll
   for (int k = 0; k < W; ++k)
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) s.dw[k][i] = 0.0f;
+    for (int i = 0; i < CPL; ++i) s.dw[k][i] = 0.0f;
 #pragma unroll
-  for (int i = 0; i < VEC; ++i) s.db[i] = 0.0f;
+  for (int i = 0; i < CPL; ++i) s.db[i] = 0.0f;
 
-  if (tile < p.tl.nT && grp < G) {
-    const int s_xt = p.s_xt, s_yt = p.s_yt;
-    const bool has_init = p.has_init;
-    const int t0 = tile * p.tl.L;
-    const int own_end = min(t0 + p.tl.L, T);
-    const int t_end = min(own_end + P, T);
-    const int emit_lo = (tile == 0 && p.need_dinit) ? -P : t0;
+  // dx of `row` (or its initial-state gradient when row < 0), plus dfinal where it applies.
+  auto emit_any = [&](int row, float (&dx)[CPL]) {
+    if (row < emit_lo) return;
+    if (dfb) {
+      const int f = row - (T - P);
+      if (f >= 0 && f < P) {
+        float d[CPL];
+        IO::unpack(IO::ld(dfb + f * D), d);
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) dx[i] += d[i];
+      }
+    }
+    if (row >= 0) DX.template st<NTS>(row, IO::pack(dx));
+    else st_vec_any<CPL>(p.dinit, state_off + (int64_t)(row + P) * D, p.i_dt, dx);
+  };
 
-    const TX* xb = static_cast<const TX*>(p.x) + (int64_t)b * p.s_xb + c0;
-    const TX* yb = static_cast<const TX*>(p.dy) + (int64_t)b * p.s_yb + c0;
-    TX* dxb = static_cast<TX*>(p.dx) + (int64_t)b * T * D + c0;
-    const int32_t* sb = SEQ ? p.seq + (int64_t)b * T : nullptr;
-    const int isz = p.i_dt == DT_F64 ? 8 : p.i_dt == DT_F32 ? 4 : 2;
-    const void* initb = has_init
-        ? static_cast<const void*>(static_cast<const char*>(p.init) + ((int64_t)b * P * D + c0) * isz)
-        : nullptr;
-    void* dinitb = p.need_dinit
-        ? static_cast<void*>(static_cast<char*>(p.dinit) + ((int64_t)b * P * D + c0) * isz)
-        : nullptr;
-    const TX* dfb = p.has_dfinal ? static_cast<const TX*>(p.dfin) + (int64_t)b * P * D + c0 : nullptr;
+  raw Ax[R], Ay[R], Bx[R], By[R];
+  int32_t As[R], Bs[R];
+  auto load = [&](raw (&bx)[R], raw (&by)[R], int32_t (&bs)[R], int t) {
+    // Rows past the end are clamped to the last row: a duplicate read keeps the number of loads in
+    // flight fixed, so the compiler's wait counts stay exact.
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(t + r, t_end - 1);
+      bx[r] = X.ld(row);
+      by[r] = Y.ld(row);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) bs[r] = SEQ ? sb[min(t + r, t_end - 1)] : 0;
+  };
 
-    load_taps<W, VEC>(p.w, p.w_dt, p.bias, p.b_dt, has_bias, c0, s.wv, s.bv);
+  float* halo_out = lds + wave * P * COLS + lane * CPL;
+  if (active) {
+    // First batch, halo rows and taps requested together.
+    const bool halo_in_x = t0 >= P;
+    raw hr[P];
+    if (halo_in_x) {
+#pragma unroll
+      for (int k = 0; k < P; ++k) hr[k] = X.ld(t0 - P + k);
+    }
+    load(Ax, Ay, As, t_main);
+    load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
 #pragma unroll
     for (int k = 0; k < P; ++k) {
       const int row = t0 - P + k;
-      load_row<TX, VEC, P>(xb, s_xt, initb, p.i_dt, has_init, D, row, s.xw[k]);
+      if (halo_in_x) IO::unpack(hr[k], s.xw[k]);
+      else if (row >= 0) IO::unpack(X.ld(row), s.xw[k]);
+      else if (has_init) ld_vec_any<CPL>(p.init, state_off + (int64_t)(row + P) * D, p.i_dt, s.xw[k]);
+      else {
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) s.xw[k][i] = 0.0f;
+      }
       s.sw[k] = SEQ ? seq_at(sb, row, T, has_init) : 0;
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) s.gw[k][i] = 0.0f;
+      for (int i = 0; i < CPL; ++i) s.gw[k][i] = 0.0f;
     }
+    // The tile's first P rows: their dx rows belong to the previous tile (or are initial-state
+    // rows), and their g values are the previous tile's right halo.
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const int t = t0 + q;
+      if (t < t_main) {
+        float dx[CPL];
+        s.step(t, X.ld(t), Y.ld(t), SEQ ? sb[t] : 0, dx);
+        emit_any(t - P, dx);
+      }
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) halo_out[q * COLS + i] = t < t_main ? s.gw[P - 1][i] : 0.0f;
+    }
+  }
+  lds_barrier();
 
-    // Stores dx of `row` (or its initial-state gradient when row < 0), adding dfinal first.
-    auto emit = [&](int row, float (&dx)[VEC]) {
-      if (dfb) {
-        const int f = row - (T - P);
-        if (f >= 0 && f < P) {
-          float d[VEC];
-          V::unpack(ld16(dfb + f * D), d);
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) dx[i] += d[i];
-        }
-      }
-      if (row >= 0) {
-        st16(dxb + row * D, V::pack(dx));
-      } else {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) st_any(dinitb, (int64_t)(row + P) * D + i, p.i_dt, dx[i]);
-      }
-    };
-
-    auto step = [&](int tt, const float (&xc)[VEC], const float (&yc)[VEC], int32_t st) {
-      float g[VEC];
-      if (SILU) {
-        float z[VEC];
-        conv_row<W, VEC, SEQ, false>(s.wv, s.bv, has_bias, s.xw, s.sw, xc, st, z);
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) g[i] = dsilu_times(yc[i], z[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) g[i] = yc[i];
-      }
-      if (SEQ && st < 0) {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) g[i] = 0.0f;
-      }
-      if (tt < own_end) {
-#pragma unroll
-        for (int k = 0; k < P; ++k) {
-          const bool m = !SEQ || s.sw[k] == st;
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) {
-            const float f = fmaf(g[i], s.xw[k][i], s.dw[k][i]);
-            s.dw[k][i] = m ? f : s.dw[k][i];
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) {
-          s.dw[P][i] = fmaf(g[i], xc[i], s.dw[P][i]);
-          s.db[i] += g[i];
-        }
-      }
-      const int row = tt - P;
-      if (row >= emit_lo) {
-        float dx[VEC];
-        s.dx_row(g, st, dx);
-        emit(row, dx);
-      }
-      shift_in(s.xw, xc);
-      shift_in(s.gw, g);
-      if (SEQ) shift_in(s.sw, st);
-    };
-
-    int t = t0;
-    for (; t + R <= t_end; t += R) {
-      uint4 rx[R], ry[R];
-      int32_t sr[R];
+  if (active) {
+    // Steady state: every step stores dx of row t - P, with t0 <= t - P < T - P.
+    auto compute = [&](const raw (&bx)[R], const raw (&by)[R], const int32_t (&bs)[R], int t) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        rx[r] = ld16(xb + (t + r) * s_xt);
-        ry[r] = ld16(yb + (t + r) * s_yt);
+        float dx[CPL];
+        s.step(t + r, bx[r], by[r], bs[r], dx);
+        DX.template st<NTS>(t + r - P, IO::pack(dx));
       }
-#pragma unroll
-      for (int r = 0; r < R; ++r) sr[r] = SEQ ? sb[t + r] : 0;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float xc[VEC], yc[VEC];
-        V::unpack(rx[r], xc);
-        V::unpack(ry[r], yc);
-        step(t + r, xc, yc, sr[r]);
-      }
+    };
+    int t = t_main;
+    for (; t + 2 * R <= t_end; t += 2 * R) {
+      load(Bx, By, Bs, t + R);
+      compute(Ax, Ay, As, t);
+      load(Ax, Ay, As, t + 2 * R);
+      compute(Bx, By, Bs, t + R);
+    }
+    if (t + R <= t_end) {
+      compute(Ax, Ay, As, t);
+      t += R;
     }
     for (; t < t_end; ++t) {
-      float xc[VEC], yc[VEC];
-      V::unpack(ld16(xb + t * s_xt), xc);
-      V::unpack(ld16(yb + t * s_yt), yc);
-      step(t, xc, yc, SEQ ? sb[t] : 0);
+      float dx[CPL];
+      s.step(t, X.ld(t), Y.ld(t), SEQ ? sb[t] : 0, dx);
+      emit_any(t - P, dx);
     }
 
-    // Rows past the end of the sequence have g = 0 and sequence id -1; they complete the last P
-    // dx rows when the tile reaches T.
-    if (t_end == T) {
-      float zero[VEC];
+    if (succ_here) {
+      // The last P dx rows, from the next wave's g of rows own_end .. own_end + P - 1.
+      const float* halo_in = lds + (wave + 1) * P * COLS + lane * CPL;
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) zero[i] = 0.0f;
+      for (int q = 0; q < P; ++q) {
+        const int tt = own_end + q;
+        float g[CPL], dx[CPL];
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) g[i] = halo_in[q * COLS + i];
+        const int32_t st = SEQ ? seq_at(sb, tt, T, has_init) : 0;
+        s.dx_row(g, st, true, dx);
+        emit_any(tt - P, dx);
+        shift_in(s.gw, g);
+        if (SEQ) shift_in(s.sw, st);
+      }
+    } else if (t_end == T) {
+      // Rows past the end of the sequence have g = 0 and sequence id -1.
+      float zero[CPL];
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) zero[i] = 0.0f;
 #pragma unroll
       for (int q = 0; q < P; ++q) {
         const int row = T + q - P;
-        if (row >= emit_lo && row < own_end) {
-          float dx[VEC];
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) dx[i] = s.wv[P][i] * s.gw[0][i];
-#pragma unroll
-          for (int j = 1; j < P; ++j) {
-            const bool m = !SEQ || s.sw[j] == s.sw[0];
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) {
-              const float f = fmaf(s.wv[P - j][i], s.gw[j][i], dx[i]);
-              dx[i] = m ? f : dx[i];
-            }
-          }
-          emit(row, dx);
+        if (row < own_end) {
+          float dx[CPL];
+          s.dx_row(zero, -1, false, dx);
+          emit_any(row, dx);
         }
         shift_in(s.gw, zero);
         if (SEQ) shift_in(s.sw, -1);
@@ -420,43 +502,40 @@ __global__ __launch_bounds__(NW * 64) void bwd_fast_kernel(const BwdParams p) {
     }
   }
 
-  // Workgroup sum of dweight/dbias in wave order 0, 1, ..., NW-1, then one partial row.
-  constexpr int COLS = 64 * VEC;
+  // Workgroup sum of dweight/dbias in wave order 0, 1, ..., NW-1, then one partial row. The halo
+  // area of LDS is reused, after every wave has read its neighbour's halo.
   if (NW > 1) {
+    lds_barrier();
     if (wave > 0) {
-      float* dst = red + (wave - 1) * (W + 1) * COLS + lane * VEC;
+      float* dst = lds + (wave - 1) * (W + 1) * COLS + lane * CPL;
 #pragma unroll
       for (int k = 0; k < W; ++k)
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) dst[k * COLS + i] = s.dw[k][i];
+        for (int i = 0; i < CPL; ++i) dst[k * COLS + i] = s.dw[k][i];
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) dst[W * COLS + i] = s.db[i];
+      for (int i = 0; i < CPL; ++i) dst[W * COLS + i] = s.db[i];
     }
-    __syncthreads();
+    lds_barrier();
   }
   if (wave == 0 && grp < G) {
 #pragma unroll 1
-    for (int wv = 1; wv < NW; ++wv) {
-      const float* src = red + (wv - 1) * (W + 1) * COLS + lane * VEC;
+    for (int v = 1; v < NW; ++v) {
+      const float* src = lds + (v - 1) * (W + 1) * COLS + lane * CPL;
 #pragma unroll
       for (int k = 0; k < W; ++k)
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) s.dw[k][i] += src[k * COLS + i];
+        for (int i = 0; i < CPL; ++i) s.dw[k][i] += src[k * COLS + i];
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) s.db[i] += src[W * COLS + i];
+      for (int i = 0; i < CPL; ++i) s.db[i] += src[W * COLS + i];
     }
-    float* pp = p.part + ((int64_t)b * p.tl.nTB + tb) * (W + 1) * D + c0;
+    float* pp = p.part + ((int64_t)tc.b * p.tl.nTB + tc.tb) * (W + 1) * D + c0;
 #pragma unroll
     for (int k = 0; k < W; ++k)
 #pragma unroll
-      for (int i = 0; i < VEC; i += 4)
-        *reinterpret_cast<float4*>(pp + k * D + i) =
-            make_float4(s.dw[k][i], s.dw[k][i + 1], s.dw[k][i + 2], s.dw[k][i + 3]);
-    if (has_bias) {
+      for (int i = 0; i < CPL; ++i) pp[k * D + i] = s.dw[k][i];
+    if (p.has_bias) {
 #pragma unroll
-      for (int i = 0; i < VEC; i += 4)
-        *reinterpret_cast<float4*>(pp + W * D + i) =
-            make_float4(s.db[i], s.db[i + 1], s.db[i + 2], s.db[i + 3]);
+      for (int i = 0; i < CPL; ++i) pp[W * D + i] = s.db[i];
     }
   }
 }

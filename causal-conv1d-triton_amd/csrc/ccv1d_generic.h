@@ -188,6 +188,7 @@ __global__ __launch_bounds__(NWR * 64) void reduce_partials_kernel(const ReduceP
   if (n < N) {
     const float* src = p.part + n;
     int q = wave;
+    // All loads of a group of 8 rows are issued before the first add.
     for (; q + 7 * NWR < p.Pn; q += 8 * NWR) {
       float v[8];
 #pragma unroll
