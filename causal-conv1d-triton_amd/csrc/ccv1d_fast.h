@@ -323,7 +323,7 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, bool NTS>
-__global__ __launch_bounds__(NW * 64) void bwd_fast_kernel(const BwdParams p) {
+__global__ __launch_bounds__(NW * 64, (W <= 5 ? 4 : 2)) void bwd_fast_kernel(const BwdParams p) {
   using IO = VecIO<TX, CPL>;
   using raw = typename IO::raw;
   constexpr int P = W - 1;

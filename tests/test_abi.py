@@ -47,10 +47,11 @@ def test_workspace_bytes():
     assert lib.ccv1d_bwd_workspace_bytes(1, 0, 8, 4, 2) == 0
     assert lib.ccv1d_bwd_workspace_bytes(1, 10, 8, 1, 2) == 0
     n = lib.ccv1d_bwd_workspace_bytes(4, 8192, 1024, 4, 2)
-    # whole fp32 partial rows of (width + 1) * dim floats
-    assert n > 0 and n % (5 * 1024 * 4) == 0
-    # never less than the generic kernel's one partial row per 64-row tile
+    # never less than the generic kernel's one fp32 partial row of (width + 1) * dim floats per
+    # 64-row tile
     assert n >= 4 * (8192 // 64) * 5 * 1024 * 4
+    # whole fp32 partial rows of (width + 1) * dim floats
+    assert n % (5 * 1024 * 4) == 0
 
 
 def _fwd(lib, **kw):

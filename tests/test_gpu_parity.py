@@ -446,3 +446,72 @@ def test_maximum_in_batch_offset():
     ref, rfin = oracle.fwd(_np32(xs), _np32(ws), final=True)
     check_lowp(_sub(out.cpu(), cols), ref, True, "out")
     assert torch.equal(_sub(fin.cpu(), cols).float(), torch.from_numpy(rfin))
+
+
+# ------------------------------------------------------------------------------------------------
+# Workspaces and graphs reused across calls.
+# ------------------------------------------------------------------------------------------------
+
+def _bwd_direct(inp, workspace):
+    from causal_conv1d_triton import _ffi
+
+    x, w, b = inp["x"].to(DEV), inp["w"].to(DEV), inp["b"].to(DEV)
+    dy = inp["dy"].to(DEV)
+    dx, dw, db = torch.empty_like(x), torch.empty_like(w), torch.empty_like(b)
+    _ffi.bwd(x, w, b, None, None, dy, None, dx, None, dw, db, workspace, True)
+    torch.cuda.synchronize()
+    return {"dx": dx.cpu(), "dw": dw.cpu(), "db": db.cpu()}
+
+
+def test_reused_workspace_with_arbitrary_contents():
+    """A reused workspace may hold anything (here an int64 arange). Results must not depend on its
+    contents and must match the oracle, call after call."""
+    from causal_conv1d_triton import _ffi
+
+    B, T, D, W = 4, 2048, 1024, 4
+    inp = make_inputs(21, B, T, D, W)
+    n = _ffi.bwd_workspace_bytes(B, T, D, W, torch.bfloat16)
+    ws = torch.arange((n + 7) // 8, dtype=torch.int64, device=DEV).view(torch.uint8)[:n]
+    ref = oracle_ref(inp, True)
+    first = _bwd_direct(inp, ws)
+    for _ in range(3):
+        again = _bwd_direct(inp, ws)
+        assert torch.equal(again["dw"], first["dw"]) and torch.equal(again["db"], first["db"])
+    check_sum(first["dw"], ref["dw"], "dweight")
+    check_sum(first["db"], ref["db"], "dbias")
+    check_lowp(first["dx"], ref["dx"], False, "dx")
+
+
+def test_graph_replays_match_eager():
+    """fwd+bwd captured in a HIP graph and replayed several times, with the program's own eager work
+    and synchronisations in between; every replay must equal the eager result bit for bit."""
+    B, T, D, W = 2, 4096, 1024, 4
+    inp = make_inputs(33, B, T, D, W, init=True)
+    x = inp["x"].to(DEV).requires_grad_(True)
+    w = inp["w"].to(DEV).requires_grad_(True)
+    b = inp["b"].to(DEV).requires_grad_(True)
+    init = inp["init"].to(DEV).requires_grad_(True)
+    dy = inp["dy"].to(DEV)
+
+    def step():
+        out = causal_conv1d_fn(x, w, b, initial_states=init, activation="silu")
+        return (out,) + torch.autograd.grad(out, (x, w, b, init), dy)
+
+    eager = [t.detach().clone() for t in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = step()
+    for rep in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for a, e in zip(outs, eager):
+            assert torch.equal(a, e), f"replay {rep}"
+        # eager work between replays, including another backward on a fresh workspace
+        other = step()
+        torch.cuda.synchronize()
+        assert torch.equal(other[2], eager[2])
