@@ -402,12 +402,19 @@ __global__ __launch_bounds__(NW * 64, (W <= 5 ? 4 : 2)) void bwd_fast_kernel(con
 
   float* halo_out = lds + wave * P * COLS + lane * CPL;
   if (active) {
-    // First batch, halo rows and taps requested together.
+    // The halo rows, the tile's first P rows, the first pipelined batch and the taps are all
+    // requested before anything waits on memory (rows past t_end are clamped to the last row).
     const bool halo_in_x = t0 >= P;
-    raw hr[P];
+    raw hr[P], px[P], py[P];
     if (halo_in_x) {
 #pragma unroll
       for (int k = 0; k < P; ++k) hr[k] = X.ld(t0 - P + k);
+    }
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const int row = min(t0 + q, t_end - 1);
+      px[q] = X.ld(row);
+      py[q] = Y.ld(row);
     }
     load(Ax, Ay, As, t_main);
     load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
@@ -432,7 +439,7 @@ __global__ __launch_bounds__(NW * 64, (W <= 5 ? 4 : 2)) void bwd_fast_kernel(con
       const int t = t0 + q;
       if (t < t_main) {
         float dx[CPL];
-        s.step(t, X.ld(t), Y.ld(t), SEQ ? sb[t] : 0, dx);
+        s.step(t, px[q], py[q], SEQ ? sb[t] : 0, dx);
         emit_any(t - P, dx);
       }
 #pragma unroll

@@ -9,19 +9,21 @@ namespace ccv1d {
 
 // Shape of the vectorised kernels per x dtype: CPL channels per lane, NW waves per workgroup, R rows
 // per pipelined batch, NTS non-temporal output stores. Chosen by measurement on MI355X (bf16,
-// B=4 T=8192 D=1024 W=4): 4 channels per lane (8-byte rows for 2-byte types) was as fast as 8 and
-// keeps the backward at 4 waves per SIMD.
+// B=4 T=8192 D=1024 W=4): the forward streams 16-byte rows with non-temporal stores; the backward
+// keeps 4 channels per lane (8-byte rows for 2-byte types), which holds it at 4 waves per SIMD, and
+// also stores non-temporally: with output buffers that change from call to call (the normal case)
+// that was faster.
 template <typename TX> struct FwdCfg {
-  static constexpr int CPL = 4;
+  static constexpr int CPL = 16 / (int)sizeof(TX);
   static constexpr int NW = 4;
   static constexpr int R = 8;
   static constexpr bool NTS = true;
 };
 template <typename TX> struct BwdCfg {
   static constexpr int CPL = 4;
-  static constexpr int NW = 8;
-  static constexpr int R = 2;
-  static constexpr bool NTS = false;
+  static constexpr int NW = 4;
+  static constexpr int R = 4;
+  static constexpr bool NTS = true;
 };
 constexpr int kMaxFastW = 8;     // widths 2..kMaxFastW have register-window kernels
 constexpr int kMaxGenericW = 128;  // LDS ring of the generic backward: 2 * W * 64 * 4 bytes
