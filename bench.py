@@ -66,6 +66,29 @@ def _time_graphs(seq, warmup):
     return start.elapsed_time(end)
 
 
+def calibrate_copy(dev, mib=256, reps=3):
+    """Plain elementwise kernels of known traffic, run so that a rocprofv3 --pmc pass over this
+    process also records FETCH_SIZE / WRITE_SIZE for kernels whose true HBM bytes are known: a fill
+    (writes mib MiB) and a negation (reads mib MiB, writes mib MiB; larger than the 256 MB Infinity
+    Cache, so its reads miss). The ratio of counter to true bytes scales the conv kernels' counters."""
+    src = torch.empty(mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the backward pass, derived from committed rocprofv3 counter runs
+    (profiles/traffic.json; written from FETCH_SIZE and WRITE_SIZE passes scaled by a plain copy of
+    known size). None when absent."""
+    path = os.path.join(_ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
 def cpu_baseline(seconds):
     """The CPU oracle (a single-threaded C restatement of the reference algorithm) on a bounded
     sample of the workload: one of the four batch rows, forward + backward, repeated for about
@@ -111,6 +134,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-eager", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run plain copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the op needs no collective (see DESIGN.md, "
@@ -132,6 +157,8 @@ def main():
         dy = torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
         sets.append((x, dy))
     torch.cuda.synchronize()
+    if args.calibrate_copy:
+        calibrate_copy(dev)
 
     def step(i):
         x, dy = sets[i]
@@ -173,6 +200,7 @@ def main():
     fwd_b, bwd_b = alg_bytes(B, T, D, W)
     gbs = (fwd_b + bwd_b) / (ms_step * 1e-3) / 1e9
     bwd_gbs = bwd_b / (ms_bwd * 1e-3) / 1e9
+    tr = traffic_from_profiles()
     line = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -196,6 +224,7 @@ def main():
                       "timed replays",
         },
         "passes_us": {"fwd": round(ms_fwd * 1e3, 2), "bwd": round(ms_bwd * 1e3, 2)},
+        "passes_gbs": {"fwd": round(fwd_b / (ms_fwd * 1e-3) / 1e9, 1), "bwd": round(bwd_gbs, 1)},
         "eager_ms_per_step": None if eager_ms is None else round(eager_ms, 4),
         "roofline": {
             "kernel": "backward pass (bwd_fast_kernel + reduce_partials_kernel)",
@@ -204,7 +233,8 @@ def main():
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(bwd_gbs / PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": None if tr is None else tr["bwd_pass_bytes"],
+            "traffic_source": None if tr is None else tr["source"],
             "alg_bytes": bwd_b,
         },
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
