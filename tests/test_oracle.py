@@ -86,3 +86,24 @@ def test_textbook_without_activation(W):
     c = pins.make_case(seed=W, B=3, T=64, D=9, W=W, init=True, dfinal=True, silu=False)
     ok, det = pins.check_textbook_no_act(c)
     assert ok, det
+
+
+@pytest.mark.parametrize("silu", [False, True])
+@pytest.mark.parametrize("bias", [False, True])
+def test_torch_cpu_baseline_matches_oracle(silu, bias):
+    """The benchmark's CPU baseline (oracle/torch_cpu.py, fp32 grouped conv1d + autograd) computes
+    the same forward and gradients as the C oracle."""
+    import numpy as np
+
+    import torch_cpu
+
+    c = pins.make_case(seed=11, B=2, T=75, D=9, W=4, bias=bias, silu=silu)
+    x, wt, b, dy = torch_cpu.prepare(c["x"], c["w"], c["b"], c["dout"])
+    out, grads = torch_cpu.fwd_bwd(x, wt, b, dy, silu)
+    ref_out, _ = pins.oracle_fwd(c)
+    dx, _, dw, db = pins.oracle_bwd(c)
+    np.testing.assert_allclose(out.detach().transpose(1, 2).numpy(), ref_out, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(grads[0].transpose(1, 2).numpy(), dx, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(grads[1][:, 0, :].numpy(), dw, rtol=1e-5, atol=1e-4)
+    if bias:
+        np.testing.assert_allclose(grads[2].numpy(), db, rtol=1e-5, atol=1e-4)
