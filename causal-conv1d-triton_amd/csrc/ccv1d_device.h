@@ -165,10 +165,18 @@ struct VecIO {
 // for the wait state a store of more than 8 bytes needs before a VALU may overwrite them, and on
 // gfx950 such stores were measured to write values of the following instructions. The compiler does
 // enforce that wait state after global stores.
-template <typename TX, int CPL>
+//
+// LD and ST are the cache-policy bits of the row loads and stores: the `aux` operand of the buffer
+// intrinsics, on gfx950 1 = sc0, 2 = nt (non-temporal), 16 = sc1. 16-byte stores, which go through a
+// global store, support the plain and the non-temporal policy only.
+constexpr int kCachePlain = 0;
+constexpr int kCacheNT = 2;
+template <typename TX, int CPL, int LD = kCachePlain, int ST = kCachePlain>
 struct RowBuf {
   using IO = VecIO<TX, CPL>;
   using raw = typename IO::raw;
+  static_assert(IO::BYTES != 16 || ST == kCachePlain || ST == kCacheNT,
+                "16-byte row stores support the plain and non-temporal policies only");
   __amdgpu_buffer_rsrc_t rs;
   const TX* base;      // row 0, channel 0 of the slab
   uint32_t lane_off;   // byte offset of this lane's first channel
@@ -182,21 +190,19 @@ struct RowBuf {
   }
   __device__ __forceinline__ raw ld(int row) const {
     if constexpr (IO::BYTES == 16)
-      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, (uint32_t)row * row_bytes, 0));
+      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, (uint32_t)row * row_bytes, LD));
     else
-      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b64(rs, lane_off, (uint32_t)row * row_bytes, 0));
+      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b64(rs, lane_off, (uint32_t)row * row_bytes, LD));
   }
-  // NT: non-temporal store (a streamed output that no later work of the kernel reads).
-  template <bool NT>
   __device__ __forceinline__ void st(int row, raw v) const {
     if constexpr (IO::BYTES == 16) {
       TX* p = reinterpret_cast<TX*>(const_cast<char*>(reinterpret_cast<const char*>(base)) +
                                     (uint64_t)((uint32_t)row * row_bytes + lane_off));
-      if (NT) IO::st_nt(p, v);
+      if (ST == kCacheNT) IO::st_nt(p, v);
       else IO::st(p, v);
     } else {
       __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), rs, lane_off,
-                                            (uint32_t)row * row_bytes, NT ? 2 : 0);
+                                            (uint32_t)row * row_bytes, ST);
     }
   }
 };

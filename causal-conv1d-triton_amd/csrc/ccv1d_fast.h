@@ -124,7 +124,7 @@ struct FwdLane {
   }
 };
 
-template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, bool NTS>
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int OST>
 __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
   using IO = VecIO<TX, CPL>;
   using raw = typename IO::raw;
@@ -142,8 +142,10 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
   const int t1 = min(t0 + p.tl.L, T);
   const bool has_init = p.has_init;
 
-  const RowBuf<TX, CPL> X(static_cast<const TX*>(p.x) + (int64_t)tc.b * p.s_xb, p.x_bytes, c0, p.s_xt);
-  const RowBuf<TX, CPL> O(static_cast<const TX*>(p.out) + (int64_t)tc.b * T * D, p.o_bytes, c0, D);
+  const RowBuf<TX, CPL, XLD> X(static_cast<const TX*>(p.x) + (int64_t)tc.b * p.s_xb, p.x_bytes, c0,
+                               p.s_xt);
+  const RowBuf<TX, CPL, kCachePlain, OST> O(static_cast<const TX*>(p.out) + (int64_t)tc.b * T * D,
+                                            p.o_bytes, c0, D);
   const int32_t* __restrict__ sb = SEQ ? p.seq + (int64_t)tc.b * T : nullptr;
   const int64_t init_off = (int64_t)tc.b * P * D + c0;
 
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
 
   auto compute = [&](const raw (&buf)[R], const int32_t (&sq)[R], int t) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) O.template st<NTS>(t + r, s.row(buf[r], sq[r]));
+    for (int r = 0; r < R; ++r) O.st(t + r, s.row(buf[r], sq[r]));
   };
 
   // Ping-pong over two register batches: batch k + 1 is in flight while batch k is computed.
@@ -201,7 +203,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
     compute(A, sA, t);
     t += R;
   }
-  for (; t < t1; ++t) O.template st<NTS>(t, s.row(X.ld(t), SEQ ? sb[t] : 0));
+  for (; t < t1; ++t) O.st(t, s.row(X.ld(t), SEQ ? sb[t] : 0));
 
   // final_states = rows T-P .. T-1 of concat(initial_states, x) (causal_conv1d.py:153-164).
   if (p.has_final && t1 == T) {
@@ -322,8 +324,16 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, bool NTS>
-__global__ __launch_bounds__(NW * 64, (W <= 5 ? 4 : 2)) void bwd_fast_kernel(const BwdParams p) {
+// Waves per SIMD the backward's register budget is sized for: 4 (128 VGPRs) for the narrow
+// instances, 2 (256 VGPRs) for widths 6..8 and for 16-byte rows at width 5.
+template <typename TX, int W, int CPL>
+constexpr int bwd_waves_per_simd() {
+  return (W <= 4 || (W == 5 && CPL * (int)sizeof(TX) <= 8)) ? 4 : 2;
+}
+
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int YLD, int DXST>
+__global__ __launch_bounds__(NW * 64, (bwd_waves_per_simd<TX, W, CPL>())) void bwd_fast_kernel(
+    const BwdParams p) {
   using IO = VecIO<TX, CPL>;
   using raw = typename IO::raw;
   constexpr int P = W - 1;
@@ -355,9 +365,9 @@ __global__ __launch_bounds__(NW * 64, (W <= 5 ? 4 : 2)) void bwd_fast_kernel(con
   const int64_t state_off = (int64_t)tc.b * P * D + c0;
   const int32_t* __restrict__ sb = SEQ ? p.seq + (int64_t)tc.b * T : nullptr;
   const TX* dfb = p.has_dfinal ? static_cast<const TX*>(p.dfin) + state_off : nullptr;
-  const RowBuf<TX, CPL> X(static_cast<const TX*>(p.x) + (int64_t)tc.b * p.s_xb, p.x_bytes, c0, p.s_xt);
-  const RowBuf<TX, CPL> Y(static_cast<const TX*>(p.dy) + (int64_t)tc.b * p.s_yb, p.y_bytes, c0, p.s_yt);
-  const RowBuf<TX, CPL> DX(static_cast<const TX*>(p.dx) + (int64_t)tc.b * T * D, p.o_bytes, c0, D);
+  const RowBuf<TX, CPL, XLD> X(static_cast<const TX*>(p.x) + (int64_t)tc.b * p.s_xb, p.x_bytes, c0, p.s_xt);
+  const RowBuf<TX, CPL, YLD> Y(static_cast<const TX*>(p.dy) + (int64_t)tc.b * p.s_yb, p.y_bytes, c0, p.s_yt);
+  const RowBuf<TX, CPL, kCachePlain, DXST> DX(static_cast<const TX*>(p.dx) + (int64_t)tc.b * T * D, p.o_bytes, c0, D);
 
   BwdLane<TX, W, SILU, SEQ, CPL> s;
   s.has_bias = p.has_bias;
@@ -381,7 +391,7 @@ __global__ __launch_bounds__(NW * 64, (W <= 5 ? 4 : 2)) void bwd_fast_kernel(con
         for (int i = 0; i < CPL; ++i) dx[i] += d[i];
       }
     }
-    if (row >= 0) DX.template st<NTS>(row, IO::pack(dx));
+    if (row >= 0) DX.st(row, IO::pack(dx));
     else st_vec_any<CPL>(p.dinit, state_off + (int64_t)(row + P) * D, p.i_dt, dx);
   };
 
@@ -455,7 +465,7 @@ __global__ __launch_bounds__(NW * 64, (W <= 5 ? 4 : 2)) void bwd_fast_kernel(con
       for (int r = 0; r < R; ++r) {
         float dx[CPL];
         s.step(t + r, bx[r], by[r], bs[r], dx);
-        DX.template st<NTS>(t + r - P, IO::pack(dx));
+        DX.st(t + r - P, IO::pack(dx));
       }
     };
     int t = t_main;

@@ -8,22 +8,26 @@
 namespace ccv1d {
 
 // Shape of the vectorised kernels per x dtype: CPL channels per lane, NW waves per workgroup, R rows
-// per pipelined batch, NTS non-temporal output stores. Chosen by measurement on MI355X (bf16,
-// B=4 T=8192 D=1024 W=4): the forward streams 16-byte rows with non-temporal stores; the backward
-// keeps 4 channels per lane (8-byte rows for 2-byte types), which holds it at 4 waves per SIMD, and
-// also stores non-temporally: with output buffers that change from call to call (the normal case)
-// that was faster.
+// per pipelined batch, and the cache policy of the row loads and stores (RowBuf). Chosen by
+// measuring whole training steps (forward then backward over rotating input sets, bf16,
+// B=4 T=8192 D=1024 W=4) on MI355X, where each pass runs right after the other; a pass timed alone
+// favours different choices. The forward keeps x cacheable, so that the backward that follows
+// finds it in the Infinity Cache, and stores out with the plain policy; the backward reads x and
+// dout non-temporally (their last use) and stores dx non-temporally.
 template <typename TX> struct FwdCfg {
-  static constexpr int CPL = 16 / (int)sizeof(TX);
+  static constexpr int CPL = 4;
   static constexpr int NW = 4;
-  static constexpr int R = 8;
-  static constexpr bool NTS = true;
+  static constexpr int R = 4;
+  static constexpr int XLD = kCachePlain;
+  static constexpr int OST = kCachePlain;
 };
 template <typename TX> struct BwdCfg {
   static constexpr int CPL = 4;
   static constexpr int NW = 4;
   static constexpr int R = 4;
-  static constexpr bool NTS = true;
+  static constexpr int XLD = kCacheNT;
+  static constexpr int YLD = kCacheNT;
+  static constexpr int DXST = kCacheNT;
 };
 constexpr int kMaxFastW = 8;     // widths 2..kMaxFastW have register-window kernels
 constexpr int kMaxGenericW = 128;  // LDS ring of the generic backward: 2 * W * 64 * 4 bytes
@@ -58,15 +62,24 @@ template <typename TX, int W, bool SILU, bool SEQ>
 static hipError_t fwd_one(const FwdParams& p, hipStream_t s) {
   using C = FwdCfg<TX>;
   return launch(reinterpret_cast<const void*>(
-                    &fwd_fast_kernel<TX, W, SILU, SEQ, C::CPL, C::NW, C::R, C::NTS>),
+                    &fwd_fast_kernel<TX, W, SILU, SEQ, C::CPL, C::NW, C::R, C::XLD, C::OST>),
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
+}
+
+// The backward's batch depth: C::R rows where the register budget of 4 waves per SIMD holds it
+// (8-byte rows, width <= 4), else 2 rows, which keeps the wider and fp32 instances from spilling.
+template <typename TX, int W>
+constexpr int bwd_rows() {
+  using C = BwdCfg<TX>;
+  return (W <= 4 && C::CPL * (int)sizeof(TX) <= 8) ? C::R : 2;
 }
 
 template <typename TX, int W, bool SILU, bool SEQ>
 static hipError_t bwd_one(const BwdParams& p, hipStream_t s) {
   using C = BwdCfg<TX>;
   return launch(reinterpret_cast<const void*>(
-                    &bwd_fast_kernel<TX, W, SILU, SEQ, C::CPL, C::NW, C::R, C::NTS>),
+                    &bwd_fast_kernel<TX, W, SILU, SEQ, C::CPL, C::NW, bwd_rows<TX, W>(), C::XLD,
+                                     C::YLD, C::DXST>),
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
 }
 
