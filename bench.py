@@ -8,6 +8,8 @@ out = causal_conv1d_fn(x, w, b, activation="silu") followed by the gradients of 
 the 256 MiB Infinity Cache) so every step reads its inputs from HBM. Steps are captured once per input
 set into one HIP graph (a replay runs one step per input set back to back) and replayed, which removes
 Python launch overhead from the device timeline; the eager (un-captured) rate is reported beside it.
+Every timed region follows at least --warmup steps and at least 50 ms of untimed replays, so it
+measures the device's steady state rather than its clock ramp after idle.
 
 Prints one JSON line. `value` is the step's algorithmic HBM bytes (read x, write out; read x, read dy,
 write dx; plus weights and bias) divided by the measured step time, in GB/s.
@@ -51,11 +53,26 @@ def _capture(fn, warm_stream):
     return g
 
 
-def _time_graphs(seq, warmup):
+# Minimum untimed device work before each timed region. MI355X raises its clocks over roughly the
+# first 10-15 ms of sustained work after any idle period of ~10 ms or more; a warm-up shorter than
+# that measures the ramp instead of the steady state.
+MIN_WARMUP_MS = 50.0
+
+
+def _warm(graph, min_replays, min_ms=MIN_WARMUP_MS):
+    """Replays `graph` at least `min_replays` times and for at least `min_ms` of wall time, without
+    leaving the device idle in between. Returns the number of replays."""
+    n, t0 = 0, time.perf_counter()
+    while n < min_replays or (time.perf_counter() - t0) * 1e3 < min_ms:
+        for _ in range(8):
+            graph.replay()
+        n += 8
+        torch.cuda.synchronize()
+    return n
+
+
+def _time_graphs(seq):
     """Device time of replaying the graphs in `seq` in order (events around the whole sequence)."""
-    for g in seq[:warmup]:
-        g.replay()
-    torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -155,8 +172,8 @@ def cpu_baseline(seconds):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--sets", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -201,8 +218,8 @@ def main():
     single = [_capture(lambda i=i: results.extend(step(i)), side) for i in range(args.sets)]
     results.clear()
     seq = [all_sets] * (args.steps // args.sets) + single[:args.steps % args.sets]
-    _time_graphs([all_sets] * max(1, args.warmup // args.sets), 0)
-    ms_step = _time_graphs(seq, 0) / args.steps
+    warm_steps = _warm(all_sets, -(-args.warmup // args.sets)) * args.sets
+    ms_step = _time_graphs(seq) / args.steps
 
     # Per-pass device time of the launches that make up a step, each pass captured on its own.
     fwd_graph = _capture(lambda: [_fwd(x.detach(), w.detach(), b.detach(), None, None, None, True)
@@ -210,8 +227,10 @@ def main():
     bwd_graph = _capture(lambda: [_bwd(x.detach(), w.detach(), b.detach(), None, None, dy, None,
                                        False, True) for x, dy in sets], side)
     reps = max(1, args.steps // args.sets)
-    ms_fwd = _time_graphs([fwd_graph] * reps, 2) / (reps * args.sets)
-    ms_bwd = _time_graphs([bwd_graph] * reps, 2) / (reps * args.sets)
+    _warm(fwd_graph, 2)
+    ms_fwd = _time_graphs([fwd_graph] * reps) / (reps * args.sets)
+    _warm(bwd_graph, 2)
+    ms_bwd = _time_graphs([bwd_graph] * reps) / (reps * args.sets)
 
     eager_ms = None
     if not args.no_eager:
@@ -235,6 +254,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warm_steps,
         "ms_per_step": round(ms_step, 5),
         "latency_us": round(ms_step * 1e3, 2),
         "frac_of_peak": round(gbs / PEAK_GBS, 4),
