@@ -14,7 +14,9 @@
 
 namespace ccv1d {
 
-// Weights (D, W) and bias (D) for channels c0 .. c0 + CPL - 1, in fp32.
+// Weights (D, W) and bias (D) for channels c0 .. c0 + CPL - 1, in fp32. Without a bias the bias
+// registers hold -0.0, which leaves every z unchanged when added (x + (-0.0) == x bit for bit, also
+// for x = +0.0 and -0.0), so the kernels add it unconditionally instead of selecting per element.
 template <int W, int CPL>
 __device__ __forceinline__ void load_taps(const void* w, int w_dt, const void* bias, int b_dt,
                                           bool has_bias, int c0, float (&wv)[W][CPL],
@@ -29,17 +31,17 @@ __device__ __forceinline__ void load_taps(const void* w, int w_dt, const void* b
     ld_vec_any<CPL>(bias, c0, b_dt, bv);
   } else {
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) bv[i] = 0.0f;
+    for (int i = 0; i < CPL; ++i) bv[i] = -0.0f;
   }
 }
 
 // Pre-activation of one row (causal_conv1d.py:129-138), in the reference's order:
 //   z = w[P] * x[t]; z = fma(w[k], x[t-P+k], z) for k = 0..P-1 (masked by sequence equality);
-//   z += bias; with ZERO_PAD, z = 0 on padding rows (sequence id < 0).
+//   z += bias (-0.0 without one); with ZERO_PAD, z = 0 on padding rows (sequence id < 0).
 // xw holds rows t-P .. t-1, sw their sequence ids; xc is row t and st its sequence id.
 template <int W, int CPL, bool SEQ, bool ZERO_PAD>
 __device__ __forceinline__ void conv_row(const float (&wv)[W][CPL], const float (&bv)[CPL],
-                                         bool has_bias, const float (&xw)[W - 1][CPL],
+                                         const float (&xw)[W - 1][CPL],
                                          const int32_t (&sw)[W - 1], const float (&xc)[CPL],
                                          int32_t st, float (&z)[CPL]) {
   constexpr int P = W - 1;
@@ -54,10 +56,8 @@ __device__ __forceinline__ void conv_row(const float (&wv)[W][CPL], const float 
       z[i] = m ? f : z[i];
     }
   }
-  if (has_bias) {
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) z[i] += bv[i];
-  }
+  for (int i = 0; i < CPL; ++i) z[i] += bv[i];
   if (SEQ && ZERO_PAD && st < 0) {
 #pragma unroll
     for (int i = 0; i < CPL; ++i) z[i] = 0.0f;
@@ -107,13 +107,12 @@ struct FwdLane {
   float bv[CPL];
   float xw[P][CPL];  // rows t-P .. t-1
   int32_t sw[P];     // their sequence ids
-  bool has_bias;
 
   // Output row t from its raw input row and sequence id.
   __device__ __forceinline__ raw row(const raw xr, int32_t st) {
     float xc[CPL], z[CPL];
     IO::unpack(xr, xc);
-    conv_row<W, CPL, SEQ, true>(wv, bv, has_bias, xw, sw, xc, st, z);
+    conv_row<W, CPL, SEQ, true>(wv, bv, xw, sw, xc, st, z);
     if (SILU) {
 #pragma unroll
       for (int i = 0; i < CPL; ++i) z[i] = z[i] * sigmoid_f(z[i]);
@@ -169,7 +168,6 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
   load(A, sA, t0);
 
   FwdLane<TX, W, SILU, SEQ, CPL> s;
-  s.has_bias = p.has_bias;
   load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
 #pragma unroll
   for (int k = 0; k < P; ++k) {
@@ -250,7 +248,6 @@ struct BwdLane {
   int32_t sw[P];      // sequence ids of rows t-P .. t-1
   float dw[W][CPL];
   float db[CPL];
-  bool has_bias;
   int own_end;
 
   // dx of row t - P, given g of row t (gt) and its sequence id (st).
@@ -285,7 +282,7 @@ struct BwdLane {
     IO::unpack(yr, g);
     if (SILU) {
       float z[CPL];
-      conv_row<W, CPL, SEQ, false>(wv, bv, has_bias, xw, sw, xc, st, z);
+      conv_row<W, CPL, SEQ, false>(wv, bv, xw, sw, xc, st, z);
 #pragma unroll
       for (int i = 0; i < CPL; ++i) g[i] = dsilu_times(g[i], z[i]);
     }
@@ -370,7 +367,6 @@ __global__ __launch_bounds__(NW * 64, (bwd_waves_per_simd<TX, W, CPL>())) void b
   const RowBuf<TX, CPL, kCachePlain, DXST> DX(static_cast<const TX*>(p.dx) + (int64_t)tc.b * T * D, p.o_bytes, c0, D);
 
   BwdLane<TX, W, SILU, SEQ, CPL> s;
-  s.has_bias = p.has_bias;
   s.own_end = own_end;
 #pragma unroll
   for (int k = 0; k < W; ++k)

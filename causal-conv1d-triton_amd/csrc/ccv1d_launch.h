@@ -23,7 +23,7 @@ template <typename TX> struct FwdCfg {
 };
 template <typename TX> struct BwdCfg {
   static constexpr int CPL = 4;
-  static constexpr int NW = 4;
+  static constexpr int NW = 8;
   static constexpr int R = 4;
   static constexpr int XLD = kCacheNT;
   static constexpr int YLD = kCacheNT;
