@@ -123,32 +123,51 @@ struct FwdLane {
   }
 };
 
-template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int OST>
-__global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
+// The same arithmetic for a walk towards earlier rows: xv holds rows t-P .. t of the output row t.
+template <typename TX, int W, bool SILU, bool SEQ, int CPL>
+struct FwdLaneRev {
+  using IO = VecIO<TX, CPL>;
+  using raw = typename IO::raw;
+  static constexpr int P = W - 1;
+  float wv[W][CPL];
+  float bv[CPL];
+  float xv[P + 1][CPL];  // rows t-P .. t
+  int32_t sv[P + 1];     // their sequence ids
+
+  // Output row t, then the window moves down one row: `xr` (row t-P-1, sequence id `st`) enters.
+  __device__ __forceinline__ raw row(const raw xr, int32_t st) {
+    float z[CPL];
+    conv_row<W, CPL, SEQ, true>(wv, bv, reinterpret_cast<const float(&)[P][CPL]>(xv),
+                                reinterpret_cast<const int32_t(&)[P]>(sv), xv[P], sv[P], z);
+    if (SILU) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) z[i] = z[i] * sigmoid_f(z[i]);
+    }
+#pragma unroll
+    for (int k = P; k > 0; --k) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) xv[k][i] = xv[k - 1][i];
+      if (SEQ) sv[k] = sv[k - 1];
+    }
+    IO::unpack(xr, xv[0]);
+    if (SEQ) sv[0] = st;
+    return IO::pack(z);
+  }
+};
+
+// One tile walked forward (rows t0 .. t1-1). Its halo rows, the first batch and the taps are requested
+// together; then a ping-pong over two register batches keeps batch k + 1 in flight while batch k is
+// computed. Rows past the tile end are clamped to its last row: a duplicate read keeps the number of
+// loads in flight independent of the tile length, so the compiler's wait counts stay exact.
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int R, int XLD, int OST>
+__device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBuf<TX, CPL, XLD>& X,
+                                                 const RowBuf<TX, CPL, kCachePlain, OST>& O,
+                                                 const int32_t* __restrict__ sb, int c0, int t0,
+                                                 int t1, int64_t init_off) {
   using IO = VecIO<TX, CPL>;
   using raw = typename IO::raw;
   constexpr int P = W - 1;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const TileCoord tc(p.tl);
-  const int tile = tc.tb * NW + wave;
-  if (tile >= p.tl.nT) return;
-  const int grp = tc.gw * 64 + lane;
-  if (grp >= p.D / CPL) return;
-  const int c0 = grp * CPL;
   const int T = p.T, D = p.D;
-  const int t0 = tile * p.tl.L;
-  const int t1 = min(t0 + p.tl.L, T);
-  const bool has_init = p.has_init;
-
-  const RowBuf<TX, CPL, XLD> X(static_cast<const TX*>(p.x) + (int64_t)tc.b * p.s_xb, p.x_bytes, c0,
-                               p.s_xt);
-  const RowBuf<TX, CPL, kCachePlain, OST> O(static_cast<const TX*>(p.out) + (int64_t)tc.b * T * D,
-                                            p.o_bytes, c0, D);
-  const int32_t* __restrict__ sb = SEQ ? p.seq + (int64_t)tc.b * T : nullptr;
-  const int64_t init_off = (int64_t)tc.b * P * D + c0;
-
-  // Halo rows, the first batch and the taps are requested together.
   const bool halo_in_x = t0 >= P;
   raw hr[P];
   if (halo_in_x) {
@@ -158,8 +177,6 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
   raw A[R], B[R];
   int32_t sA[R], sB[R];
   auto load = [&](raw (&buf)[R], int32_t (&sq)[R], int t) {
-    // Rows past the tile end are clamped to its last row: a duplicate read keeps the number of
-    // loads in flight independent of the tile length, so the compiler's wait counts stay exact.
 #pragma unroll
     for (int r = 0; r < R; ++r) buf[r] = X.ld(min(t + r, t1 - 1));
 #pragma unroll
@@ -175,21 +192,19 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
     else {
       const int row = t0 - P + k;
       if (row >= 0) IO::unpack(X.ld(row), s.xw[k]);
-      else if (has_init) ld_vec_any<CPL>(p.init, init_off + (int64_t)(row + P) * D, p.i_dt, s.xw[k]);
+      else if (p.has_init) ld_vec_any<CPL>(p.init, init_off + (int64_t)(row + P) * D, p.i_dt, s.xw[k]);
       else {
 #pragma unroll
         for (int i = 0; i < CPL; ++i) s.xw[k][i] = 0.0f;
       }
     }
-    s.sw[k] = SEQ ? seq_at(sb, t0 - P + k, T, has_init) : 0;
+    s.sw[k] = SEQ ? seq_at(sb, t0 - P + k, T, p.has_init) : 0;
   }
 
   auto compute = [&](const raw (&buf)[R], const int32_t (&sq)[R], int t) {
 #pragma unroll
     for (int r = 0; r < R; ++r) O.st(t + r, s.row(buf[r], sq[r]));
   };
-
-  // Ping-pong over two register batches: batch k + 1 is in flight while batch k is computed.
   int t = t0;
   for (; t + 2 * R <= t1; t += 2 * R) {
     load(B, sB, t + R);
@@ -202,6 +217,90 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
     t += R;
   }
   for (; t < t1; ++t) O.st(t, s.row(X.ld(t), SEQ ? sb[t] : 0));
+}
+
+// One tile walked backward (outputs t1-1 down to t0), for tiles with t0 >= 16 > P, whose rows all
+// lie in x. The window starts as rows t1-1-P .. t1-1; output t then takes in row t-P-1. Rows below
+// t0-P are clamped to t0-P, for the same reason as the clamp of the forward walk.
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int R, int XLD, int OST>
+__device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBuf<TX, CPL, XLD>& X,
+                                                 const RowBuf<TX, CPL, kCachePlain, OST>& O,
+                                                 const int32_t* __restrict__ sb, int c0, int t0,
+                                                 int t1) {
+  using IO = VecIO<TX, CPL>;
+  using raw = typename IO::raw;
+  constexpr int P = W - 1;
+  const int lo = t0 - P;
+  raw wr[P + 1];
+#pragma unroll
+  for (int k = 0; k <= P; ++k) wr[k] = X.ld(t1 - 1 - P + k);
+  raw A[R], B[R];
+  int32_t sA[R], sB[R];
+  auto load = [&](raw (&buf)[R], int32_t (&sq)[R], int row) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) buf[r] = X.ld(max(row - r, lo));
+#pragma unroll
+    for (int r = 0; r < R; ++r) sq[r] = SEQ ? sb[max(row - r, lo)] : 0;
+  };
+  load(A, sA, t1 - 2 - P);
+
+  FwdLaneRev<TX, W, SILU, SEQ, CPL> s;
+  load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
+#pragma unroll
+  for (int k = 0; k <= P; ++k) {
+    IO::unpack(wr[k], s.xv[k]);
+    s.sv[k] = SEQ ? sb[t1 - 1 - P + k] : 0;
+  }
+
+  auto compute = [&](const raw (&buf)[R], const int32_t (&sq)[R], int t) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) O.st(t - r, s.row(buf[r], sq[r]));
+  };
+  int t = t1 - 1;  // next output row
+  for (; t - 2 * R + 1 >= t0; t -= 2 * R) {
+    load(B, sB, t - R - P - 1);
+    compute(A, sA, t);
+    load(A, sA, t - 2 * R - P - 1);
+    compute(B, sB, t - R);
+  }
+  if (t - R + 1 >= t0) {
+    compute(A, sA, t);
+    t -= R;
+  }
+  for (; t >= t0; --t) {
+    const int row = max(t - P - 1, lo);
+    O.st(t, s.row(X.ld(row), SEQ ? sb[row] : 0));
+  }
+}
+
+// Even tiles walk forward and odd tiles backward. A tile's last P rows are the next tile's halo:
+// with alternating directions both tiles read those rows at about the same time (both at their
+// start, or both at their end), so the second read finds them in L2 instead of memory.
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int OST>
+__global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
+  using IO = VecIO<TX, CPL>;
+  constexpr int P = W - 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const TileCoord tc(p.tl);
+  const int tile = tc.tb * NW + wave;
+  if (tile >= p.tl.nT) return;
+  const int grp = tc.gw * 64 + lane;
+  if (grp >= p.D / CPL) return;
+  const int c0 = grp * CPL;
+  const int T = p.T, D = p.D;
+  const int t0 = tile * p.tl.L;
+  const int t1 = min(t0 + p.tl.L, T);
+
+  const RowBuf<TX, CPL, XLD> X(static_cast<const TX*>(p.x) + (int64_t)tc.b * p.s_xb, p.x_bytes, c0,
+                               p.s_xt);
+  const RowBuf<TX, CPL, kCachePlain, OST> O(static_cast<const TX*>(p.out) + (int64_t)tc.b * T * D,
+                                            p.o_bytes, c0, D);
+  const int32_t* __restrict__ sb = SEQ ? p.seq + (int64_t)tc.b * T : nullptr;
+  const int64_t init_off = (int64_t)tc.b * P * D + c0;
+
+  if (tile & 1) fwd_tile_reverse<TX, W, SILU, SEQ, CPL, R>(p, X, O, sb, c0, t0, t1);
+  else fwd_tile_forward<TX, W, SILU, SEQ, CPL, R>(p, X, O, sb, c0, t0, t1, init_off);
 
   // final_states = rows T-P .. T-1 of concat(initial_states, x) (causal_conv1d.py:153-164).
   if (p.has_final && t1 == T) {
@@ -211,7 +310,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
       const int row = T - P + q;
       float f[CPL];
       if (row >= 0) IO::unpack(X.ld(row), f);
-      else if (has_init) ld_vec_any<CPL>(p.init, init_off + (int64_t)(row + P) * D, p.i_dt, f);
+      else if (p.has_init) ld_vec_any<CPL>(p.init, init_off + (int64_t)(row + P) * D, p.i_dt, f);
       else {
 #pragma unroll
         for (int i = 0; i < CPL; ++i) f[i] = 0.0f;
