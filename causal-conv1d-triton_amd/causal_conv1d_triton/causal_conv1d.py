@@ -65,6 +65,92 @@ def _bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, need_din
     return dx, dweight, dbias, dinit
 
 
+# ---------------------------------------------------------------------------------------------
+# The two passes as torch.library custom operators, so that torch.compile traces
+# causal_conv1d_fn without a graph break (the reference keeps its host code dynamo-friendly,
+# causal_conv1d.py:386-394). The fake implementations give output shapes and dtypes; autograd is
+# registered on the forward operator. Absent optional outputs are returned as empty tensors.
+# ---------------------------------------------------------------------------------------------
+
+
+@torch.library.custom_op("causal_conv1d_amd::fwd", mutates_args=(), device_types="cuda")
+def _fwd_op(
+    x: Tensor,
+    weight: Tensor,
+    bias: Tensor | None,
+    seq_idx: Tensor | None,
+    initial_states: Tensor | None,
+    return_final_states: bool,
+    silu: bool,
+) -> tuple[Tensor, Tensor]:
+    B, T, D = x.shape
+    if return_final_states:
+        final_states = torch.empty(B, weight.shape[1] - 1, D, device=x.device, dtype=x.dtype)
+    else:
+        final_states = x.new_empty(0)
+    out = _fwd(x, weight, bias, seq_idx, initial_states,
+               final_states if return_final_states else None, silu)
+    return out, final_states
+
+
+@_fwd_op.register_fake
+def _fwd_fake(x, weight, bias, seq_idx, initial_states, return_final_states, silu):
+    B, T, D = x.shape
+    out = x.new_empty(B, T, D)
+    final_states = x.new_empty(B, weight.shape[1] - 1, D) if return_final_states else x.new_empty(0)
+    return out, final_states
+
+
+@torch.library.custom_op("causal_conv1d_amd::bwd", mutates_args=(), device_types="cuda")
+def _bwd_op(
+    x: Tensor,
+    weight: Tensor,
+    bias: Tensor | None,
+    seq_idx: Tensor | None,
+    initial_states: Tensor | None,
+    dout: Tensor,
+    dfinal_states: Tensor | None,
+    need_dinit: bool,
+    silu: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    dx, dweight, dbias, dinit = _bwd(x, weight, bias, seq_idx, initial_states, dout,
+                                     dfinal_states, need_dinit, silu)
+    return (dx, dweight, dbias if dbias is not None else x.new_empty(0),
+            dinit if dinit is not None else x.new_empty(0))
+
+
+@_bwd_op.register_fake
+def _bwd_fake(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, need_dinit, silu):
+    B, T, D = x.shape
+    dbias = bias.new_empty(bias.shape) if bias is not None else x.new_empty(0)
+    dinit = initial_states.new_empty(initial_states.shape) if need_dinit else x.new_empty(0)
+    return x.new_empty(B, T, D), weight.new_empty(weight.shape), dbias, dinit
+
+
+def _fwd_op_setup_context(ctx, inputs, output):
+    x, weight, bias, seq_idx, initial_states, return_final_states, silu = inputs
+    ctx.save_for_backward(x, weight, bias, seq_idx, initial_states)
+    ctx.silu = silu
+    ctx.return_final_states = return_final_states
+
+
+def _fwd_op_backward(ctx, dout, dfinal_states):
+    x, weight, bias, seq_idx, initial_states = ctx.saved_tensors
+    need_dinit = initial_states is not None and ctx.needs_input_grad[4]
+    if not ctx.return_final_states or dfinal_states is None:
+        dfinal_states = None
+    else:
+        dfinal_states = dfinal_states.contiguous()
+    dx, dweight, dbias, dinit = _bwd_op(x, weight, bias, seq_idx, initial_states,
+                                        _channels_contiguous(dout), dfinal_states, need_dinit,
+                                        ctx.silu)
+    return (dx, dweight, dbias if bias is not None else None, None,
+            dinit if need_dinit else None, None, None)
+
+
+_fwd_op.register_autograd(_fwd_op_backward, setup_context=_fwd_op_setup_context)
+
+
 class _CausalConv1dFn(torch.autograd.Function):
     """Autograd wiring of the reference (causal_conv1d.py:544-576): saves the inputs (not the
     output) and recomputes the pre-activation in backward."""
@@ -147,7 +233,12 @@ def causal_conv1d_fn(
     needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (x, weight, bias, initial_states)
     )
-    if needs_grad:
+    if torch.compiler.is_compiling():
+        # Under torch.compile the passes go through the registered custom operators.
+        out, final_states = _fwd_op(x, weight, bias, seq_idx, initial_states, return_final_states,
+                                    silu)
+        result = (out, final_states) if return_final_states else out
+    elif needs_grad:
         result = _CausalConv1dFn.apply(
             x, weight, bias, seq_idx, initial_states, return_final_states, silu
         )

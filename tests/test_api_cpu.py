@@ -80,3 +80,28 @@ def test_ffi_refuses_unsupported_dtype():
 
     with pytest.raises(TypeError):
         _ffi._code(torch.zeros(1, dtype=torch.int32))
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("init", [False, True])
+@pytest.mark.parametrize("final", [False, True])
+def test_custom_op_fake_shapes(bias, init, final):
+    """The torch.library operators (used under torch.compile) report the shapes and dtypes of the
+    tensors the kernels write, checked with fake CUDA tensors (no device needed)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    B, T, D, W = 2, 33, 24, 4
+    with FakeTensorMode():
+        x = torch.empty(B, T, D, device="cuda", dtype=torch.bfloat16)
+        w = torch.empty(D, W, device="cuda", dtype=torch.float32)
+        b = torch.empty(D, device="cuda", dtype=torch.float16) if bias else None
+        s0 = torch.empty(B, W - 1, D, device="cuda", dtype=torch.float32) if init else None
+        out, fin = torch.ops.causal_conv1d_amd.fwd(x, w, b, None, s0, final, True)
+        assert out.shape == (B, T, D) and out.dtype == x.dtype and out.device == x.device
+        assert fin.shape == ((B, W - 1, D) if final else (0,))
+        dfin = torch.empty(B, W - 1, D, device="cuda", dtype=x.dtype) if final else None
+        dx, dw, db, di = torch.ops.causal_conv1d_amd.bwd(x, w, b, None, s0, out, dfin, init, True)
+        assert dx.shape == x.shape and dx.dtype == x.dtype
+        assert dw.shape == w.shape and dw.dtype == w.dtype
+        assert db.shape == ((D,) if bias else (0,)) and (not bias or db.dtype == b.dtype)
+        assert di.shape == ((B, W - 1, D) if init else (0,)) and (not init or di.dtype == s0.dtype)
