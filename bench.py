@@ -17,6 +17,7 @@ write dx; plus weights and bias) divided by the measured step time, in GB/s.
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -169,6 +170,155 @@ def cpu_baseline(seconds):
     return out
 
 
+def _alg_bytes_general(B, T, D, W, bias, init=False, seq=False, final=False, ex=2, ew=4, eb=4,
+                       ei=2):
+    """Algorithmic HBM bytes of a forward and of a backward pass with the optional tensors: weights
+    and bias read once per pass, dweight/dbias written once; initial states read (and their gradient
+    written), final states written, seq_idx read in each pass."""
+    n = B * T * D
+    st = B * (W - 1) * D
+    fwd = n * 2 * ex + D * W * ew + (D * eb if bias else 0) + (st * ei if init else 0)
+    fwd += (st * ex if final else 0) + (B * T * 4 if seq else 0)
+    bwd = n * 3 * ex + 2 * D * W * ew + (2 * D * eb if bias else 0)
+    bwd += (2 * st * ei if init else 0) + (B * T * 4 if seq else 0)
+    return fwd, bwd
+
+
+def run_configs(dev):
+    """One JSON line per BASELINE configuration 2-5 (the reference's README sweep, the Mamba-2 xBC
+    shape, chunked streaming and decode with state handoff, packed varlen seq_idx): device time per
+    call from replayed graphs after the usual warm-up, plus, for the latency-bound streaming and
+    decode calls, the host-inclusive eager time per call."""
+    from causal_conv1d_triton import causal_conv1d_fn
+    from causal_conv1d_triton.causal_conv1d import _fwd
+
+    side = torch.cuda.Stream()
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    def emit(name, shape, us, fb, bb, kind, extra=None):
+        line = {"config": name, "shape": shape, "pass": kind, "latency_us": round(us, 2)}
+        nbytes = fb if kind == "fwd" else fb + bb
+        if nbytes:
+            line["gbs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+            line["frac_of_peak"] = round(nbytes / (us * 1e-6) / 1e9 / PEAK_GBS, 4)
+        if extra:
+            line.update(extra)
+        print(json.dumps(line), flush=True)
+
+    def timed(graph, per_replay):
+        _warm(graph, 2)
+        reps = 20
+        return _time_graphs([graph] * reps) / (reps * per_replay) * 1e3
+
+    def steps(sets, w, b, act, init=None, seq=None, xs=None):
+        res = []
+
+        def fn():
+            for i, (x, dy) in enumerate(sets):
+                xi = x if xs is None else xs[i]
+                out = causal_conv1d_fn(xi, w, b, seq_idx=seq, initial_states=init, activation=act)
+                grads = [t for t in (xi, w, b, init) if t is not None and t.requires_grad]
+                res.append(torch.autograd.grad(out, grads, dy))
+        g = _capture(fn, side)
+        res.clear()
+        return g
+
+    def fwds(sets, w, b, act):
+        res = []
+
+        def fn():
+            for x, _ in sets:
+                res.append(_fwd(x.detach(), w.detach(), None if b is None else b.detach(), None,
+                                None, None, act is not None))
+        g = _capture(fn, side)
+        res.clear()
+        return g
+
+    # Configuration 2: README shape sweep, B=4 D=1024 W=4, weight only or bias + silu.
+    for T in (512, 2048, 8192, 32768):
+        B, D, W = 4, 1024, 4
+        nsets = max(2, min(8, (512 << 20) // (2 * B * T * D * 2)))
+        sets = [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
+                 .requires_grad_(True),
+                 torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
+                for _ in range(nsets)]
+        w = (torch.randn(D, W, generator=gen, device=dev) / 2).requires_grad_(True)
+        for variant in ("weight_only", "bias_silu"):
+            bias = variant == "bias_silu"
+            b = torch.randn(D, generator=gen, device=dev).requires_grad_(True) if bias else None
+            act = "silu" if bias else None
+            fb, bb = _alg_bytes_general(B, T, D, W, bias)
+            shape = f"B={B} T={T} D={D} W={W} {variant}"
+            emit("2", shape, timed(fwds(sets, w, b, act), nsets), fb, bb, "fwd")
+            emit("2", shape, timed(steps(sets, w, b, act), nsets), fb, bb, "fwd+bwd")
+        del sets
+    # Configuration 3: Mamba-2 2.7B xBC, x a channel slice of an in_proj output.
+    B, T, D, W = 8, 4096, 5376, 4
+    bigs = [torch.randn(B, T, 10576, generator=gen, device=dev).to(torch.bfloat16) for _ in range(2)]
+    xs = [bg[..., 5120:5120 + D].detach().requires_grad_(True) for bg in bigs]
+    sets = [(x, torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)) for x in xs]
+    w = (torch.rand(D, W, generator=gen, device=dev) - 0.5).requires_grad_(True)
+    b = ((torch.rand(D, generator=gen, device=dev) - 0.5) * 0.2).requires_grad_(True)
+    fb, bb = _alg_bytes_general(B, T, D, W, True)
+    emit("3", f"B={B} T={T} D={D} W={W} x=slice(in_proj, stride 10576)",
+         timed(steps(sets, w, b, "silu", xs=xs), 2), fb, bb, "fwd+bwd")
+    del bigs, xs, sets
+    # Configuration 4: streaming, B=16 D=2048 W=4, T=8192 as 32 chunks of 256 with state handoff,
+    # and decode steps of T=1.
+    B, T, D, W = 16, 8192, 2048, 4
+    x = torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
+    w = torch.randn(D, W, generator=gen, device=dev) / 2
+    b = torch.randn(D, generator=gen, device=dev)
+    for name, chunk, n in (("chunk", 256, 32), ("decode", 1, 64)):
+        def stream_fn():
+            state = None
+            for c in range(n):
+                _, state = causal_conv1d_fn(x[:, c * chunk:(c + 1) * chunk], w, b,
+                                            initial_states=state, return_final_states=True,
+                                            activation="silu")
+        with torch.no_grad():
+            g = _capture(stream_fn, side)
+            dev_us = timed(g, n)
+            for _ in range(3):
+                stream_fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            reps = 20
+            for _ in range(reps):
+                stream_fn()
+            torch.cuda.synchronize()
+            host_us = (time.perf_counter() - t0) * 1e6 / (reps * n)
+        fb, _ = _alg_bytes_general(B, chunk, D, W, True, init=True, final=True)
+        emit("4", f"B={B} D={D} W={W} {name} T={chunk} x{n}, state handoff", dev_us, fb, 0, "fwd",
+             {"eager_us_per_call": round(host_us, 2)})
+    del x
+    # Configuration 5: packed varlen seq_idx, B=4 T=16384 D=4096, W in {4, 7}, initial states.
+    B, T, D = 4, 16384, 4096
+    seq = torch.empty(B, T, dtype=torch.int32)
+    gs = torch.Generator().manual_seed(5)
+    for bb_ in range(B):
+        t, sid = 0, 0
+        while t < T:
+            n = int(torch.randint(64, 4097, (1,), generator=gs))
+            seq[bb_, t:t + n] = sid
+            t, sid = t + n, sid + 1
+        seq[bb_, T - int(0.05 * T):] = -1
+    seq = seq.to(dev)
+    for W in (4, 7):
+        sets = [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
+                 .requires_grad_(True),
+                 torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
+                for _ in range(2)]
+        w = (torch.randn(D, W, generator=gen, device=dev) / math.sqrt(W)).requires_grad_(True)
+        b = torch.randn(D, generator=gen, device=dev).requires_grad_(True)
+        init = torch.randn(B, W - 1, D, generator=gen, device=dev).to(torch.bfloat16)
+        init.requires_grad_(True)
+        fb, bb = _alg_bytes_general(B, T, D, W, True, init=True, seq=True)
+        emit("5", f"B={B} T={T} D={D} W={W} seq_idx varlen, initial_states",
+             timed(steps(sets, w, b, "silu", init=init, seq=seq), 2), fb, bb, "fwd+bwd")
+        del sets
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -178,6 +328,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-eager", action="store_true")
+    ap.add_argument("--configs", action="store_true",
+                    help="instead of the headline line, one JSON line per BASELINE configuration 2-5")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -191,6 +343,9 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.configs:
+        run_configs(dev)
+        return
     B, T, D, W = 4, 8192, 1024, 4
     gen = torch.Generator(device=dev).manual_seed(0)
     w = (torch.randn(D, W, generator=gen, device=dev) / 2).requires_grad_(True)
