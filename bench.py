@@ -7,7 +7,8 @@ out = causal_conv1d_fn(x, w, b, activation="silu") followed by the gradients of 
 (torch.autograd.grad, so nothing is accumulated). Input sets rotate (4 sets of x and dy, 512 MiB, twice
 the 256 MiB Infinity Cache) so every step reads its inputs from HBM. Steps are captured once per input
 set into one HIP graph (a replay runs one step per input set back to back) and replayed, which removes
-Python launch overhead from the device timeline; the eager (un-captured) rate is reported beside it.
+Python launch overhead from the device timeline. The time of each pass inside the step (the roofline
+entry) comes from events between the passes of eager steps that make the same launches.
 Every timed region follows at least --warmup steps and at least 50 ms of untimed replays, so it
 measures the device's steady state rather than its clock ramp after idle.
 
@@ -82,6 +83,72 @@ def _time_graphs(seq):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end)
+
+
+def passes_in_step(sets, w, b, steps):
+    """Mean device time of the forward and of the backward pass inside fwd+bwd steps, and of the
+    step. The steps run eagerly through the launches causal_conv1d_fn and its autograd backward make
+    (_fwd, then _bwd: the same kernels on the same stream), with HIP events on the launch stream
+    before the forward, between the passes and after the backward. All measured steps are queued
+    behind a bounded spin kernel (torch.cuda._sleep) that keeps the device busy while the host
+    enqueues them, so the device then runs them back to back without waiting for the host and each
+    event interval is device time only. Returns {"fwd": ms, "bwd": ms, "step": ms}."""
+    from causal_conv1d_triton.causal_conv1d import _bwd, _fwd
+
+    n = len(sets)
+    wd, bd = w.detach(), b.detach()
+
+    def step(i, ev=None):
+        x, dy = sets[i % n]
+        if ev:
+            ev[0].record()
+        _fwd(x.detach(), wd, bd, None, None, None, True)
+        if ev:
+            ev[1].record()
+        r = _bwd(x.detach(), wd, bd, None, None, dy, None, False, True)
+        if ev:
+            ev[2].record()
+        return r
+
+    # spin-kernel cycles per millisecond on this device
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record()
+    torch.cuda._sleep(1 << 20)
+    s1.record()
+    torch.cuda.synchronize()
+    cycles_per_ms = (1 << 20) / max(s0.elapsed_time(s1), 1e-3)
+    # host time to enqueue one step, measured on the warm-up steps
+    k, t0 = 0, time.perf_counter()
+    while k < 2 * n or (time.perf_counter() - t0) * 1e3 < MIN_WARMUP_MS:
+        step(k)
+        k += 1
+        if k % 32 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - t0) * 1e3 / k
+    # Events on every EVERY-th step only: an event between two launches costs the device time of
+    # its own, which the other steps then do not pay.
+    every = 4
+    steps = max(steps, 2 * every)
+    evs = {i: [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+           for i in range(steps) if i % every == every - 1}
+    first, last = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # queue some warm steps, then the spin, then the measured steps, so the device is busy and warm
+    for i in range(16):
+        step(i)
+    torch.cuda._sleep(int(cycles_per_ms * (2 * host_ms * steps + 5)))
+    skip = 4 * every  # steps right after the spin, while clocks ramp up again
+    for i in range(steps + skip):
+        if i == skip:
+            first.record()
+        step(i, evs.get(i - skip))
+    last.record()
+    torch.cuda.synchronize()
+    use = list(evs.values())
+    fwd = sum(e[0].elapsed_time(e[1]) for e in use) / len(use)
+    bwd = sum(e[1].elapsed_time(e[2]) for e in use) / len(use)
+    step_ms = first.elapsed_time(last) / steps
+    return {"fwd": fwd, "bwd": bwd, "step": step_ms}
 
 
 def calibrate_copy(dev, mib=256, reps=3):
@@ -327,7 +394,8 @@ def main():
     ap.add_argument("--sets", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-eager", action="store_true")
+    ap.add_argument("--isolated", action="store_true",
+                    help="also time each pass alone (graphs of one pass per input set)")
     ap.add_argument("--configs", action="store_true",
                     help="instead of the headline line, one JSON line per BASELINE configuration 2-5")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -376,31 +444,24 @@ def main():
     warm_steps = _warm(all_sets, -(-args.warmup // args.sets)) * args.sets
     ms_step = _time_graphs(seq) / args.steps
 
-    # Per-pass device time of the launches that make up a step, each pass captured on its own.
-    fwd_graph = _capture(lambda: [_fwd(x.detach(), w.detach(), b.detach(), None, None, None, True)
-                                  for x, _ in sets], side)
-    bwd_graph = _capture(lambda: [_bwd(x.detach(), w.detach(), b.detach(), None, None, dy, None,
-                                       False, True) for x, dy in sets], side)
-    reps = max(1, args.steps // args.sets)
-    _warm(fwd_graph, 2)
-    ms_fwd = _time_graphs([fwd_graph] * reps) / (reps * args.sets)
-    _warm(bwd_graph, 2)
-    ms_bwd = _time_graphs([bwd_graph] * reps) / (reps * args.sets)
+    # Per-pass device time inside the step (events between the passes of eager steps).
+    ms_pass = passes_in_step(sets, w, b, args.steps)
+    ms_fwd, ms_bwd = ms_pass["fwd"], ms_pass["bwd"]
 
-    eager_ms = None
-    if not args.no_eager:
-        k, t0 = 0, time.perf_counter()
-        while k < args.warmup or (time.perf_counter() - t0) * 1e3 < MIN_WARMUP_MS:
-            step(k % args.sets)
-            k += 1
-            if k % 32 == 0:
-                torch.cuda.synchronize()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for k in range(args.steps):
-            step(k % args.sets)
-        torch.cuda.synchronize()
-        eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    isolated = None
+    if args.isolated:
+        # Each pass captured on its own and replayed back to back (the other pass does not run, so
+        # neither finds the other's data in the Infinity Cache).
+        fwd_graph = _capture(lambda: [_fwd(x.detach(), w.detach(), b.detach(), None, None, None,
+                                           True) for x, _ in sets], side)
+        bwd_graph = _capture(lambda: [_bwd(x.detach(), w.detach(), b.detach(), None, None, dy,
+                                           None, False, True) for x, dy in sets], side)
+        reps = max(1, args.steps // args.sets)
+        _warm(fwd_graph, 2)
+        iso_fwd = _time_graphs([fwd_graph] * reps) / (reps * args.sets)
+        _warm(bwd_graph, 2)
+        iso_bwd = _time_graphs([bwd_graph] * reps) / (reps * args.sets)
+        isolated = {"fwd": round(iso_fwd * 1e3, 2), "bwd": round(iso_bwd * 1e3, 2)}
 
     fwd_b, bwd_b = alg_bytes(B, T, D, W)
     gbs = (fwd_b + bwd_b) / (ms_step * 1e-3) / 1e9
@@ -429,13 +490,15 @@ def main():
             "timing": "one hip graph of one step per input set, replayed; events around the "
                       "timed replays",
         },
-        "passes_isolated_us": {"fwd": round(ms_fwd * 1e3, 2), "bwd": round(ms_bwd * 1e3, 2)},
-        "passes_isolated_gbs": {"fwd": round(fwd_b / (ms_fwd * 1e-3) / 1e9, 1),
-                                "bwd": round(bwd_gbs, 1)},
-        "eager_ms_per_step": None if eager_ms is None else round(eager_ms, 4),
+        "passes_in_step_us": {"fwd": round(ms_fwd * 1e3, 2), "bwd": round(ms_bwd * 1e3, 2)},
+        "passes_in_step_gbs": {"fwd": round(fwd_b / (ms_fwd * 1e-3) / 1e9, 1),
+                               "bwd": round(bwd_gbs, 1)},
+        "eager_step_us": round(ms_pass["step"] * 1e3, 2),
+        "passes_isolated_us": isolated,
         "roofline": {
             "kernel": "backward pass (bwd_fast_kernel + reduce_partials_kernel)",
-            "measured": "events around replays of a graph of backward passes (one per input set)",
+            "measured": "HIP events on the launch stream around the backward pass of every 4th "
+                        f"of {args.steps} eager fwd+bwd steps queued back to back (mean)",
             "launch_us": round(ms_bwd * 1e3, 2),
             "bound": "hbm",
             "achieved": round(bwd_gbs, 1),

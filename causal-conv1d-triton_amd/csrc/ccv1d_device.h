@@ -167,10 +167,13 @@ struct VecIO {
 // enforce that wait state after global stores.
 //
 // LD and ST are the cache-policy bits of the row loads and stores: the `aux` operand of the buffer
-// intrinsics, on gfx950 1 = sc0, 2 = nt (non-temporal), 16 = sc1. 16-byte stores, which go through a
-// global store, support the plain and the non-temporal policy only.
+// intrinsics, on gfx950 1 = sc0, 2 = nt (non-temporal), 16 = sc1 (device scope: the store is written
+// through the L2 instead of staying there dirty until the end of the kernel). 16-byte stores, which
+// go through a global store, support the plain and the non-temporal policy only.
 constexpr int kCachePlain = 0;
 constexpr int kCacheNT = 2;
+constexpr int kCacheSC1 = 16;
+constexpr int kCacheSC1NT = kCacheSC1 | kCacheNT;
 template <typename TX, int CPL, int LD = kCachePlain, int ST = kCachePlain>
 struct RowBuf {
   using IO = VecIO<TX, CPL>;

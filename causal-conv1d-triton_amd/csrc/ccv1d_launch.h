@@ -11,15 +11,18 @@ namespace ccv1d {
 // per pipelined batch, and the cache policy of the row loads and stores (RowBuf). Chosen by
 // measuring whole training steps (forward then backward over rotating input sets, bf16,
 // B=4 T=8192 D=1024 W=4) on MI355X, where each pass runs right after the other; a pass timed alone
-// favours different choices. The forward keeps x cacheable, so that the backward that follows
-// finds it in the Infinity Cache, and stores out with the plain policy; the backward reads x and
-// dout non-temporally (their last use) and stores dx non-temporally.
+// favours different choices, because each pass's policies decide what the other finds in the
+// Infinity Cache. The forward keeps x cacheable, so that the backward that follows finds it in the
+// Infinity Cache, and writes out through the L2 at device scope (sc1), which leaves little dirty
+// data for the L2 write-back at the end of the kernel; the backward reads x and dout non-temporally
+// (their last use) and stores dx non-temporally at device scope. 16-byte rows (fp32) keep the plain
+// and non-temporal stores their global-store path supports.
 template <typename TX> struct FwdCfg {
   static constexpr int CPL = 4;
-  static constexpr int NW = 4;
+  static constexpr int NW = 8;
   static constexpr int R = 4;
   static constexpr int XLD = kCachePlain;
-  static constexpr int OST = kCachePlain;
+  static constexpr int OST = sizeof(TX) == 2 ? kCacheSC1 : kCachePlain;
 };
 template <typename TX> struct BwdCfg {
   static constexpr int CPL = 4;
@@ -27,7 +30,7 @@ template <typename TX> struct BwdCfg {
   static constexpr int R = 4;
   static constexpr int XLD = kCacheNT;
   static constexpr int YLD = kCacheNT;
-  static constexpr int DXST = kCacheNT;
+  static constexpr int DXST = sizeof(TX) == 2 ? kCacheSC1NT : kCacheNT;
 };
 constexpr int kMaxFastW = 8;     // widths 2..kMaxFastW have register-window kernels
 constexpr int kMaxGenericW = 128;  // LDS ring of the generic backward: 2 * W * 64 * 4 bytes
