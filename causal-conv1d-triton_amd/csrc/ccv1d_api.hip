@@ -107,8 +107,21 @@ Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
   return t;
 }
 
-Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
-  const FastShape sh = shape_of<BwdCfg>(x_dt);
+// Channels per lane and waves per workgroup of the vectorised backward at width W.
+FastShape bwd_shape(int x_dt, int64_t W) {
+  FastShape sh = shape_of<BwdCfg>(x_dt);
+  if (W >= kBwdWideW) {
+    switch (x_dt) {
+      case CCV1D_BF16: sh.cpl = BwdCfg<__bf16>::CPL_WIDE; break;
+      case CCV1D_F16: sh.cpl = BwdCfg<_Float16>::CPL_WIDE; break;
+      default: sh.cpl = BwdCfg<float>::CPL_WIDE; break;
+    }
+  }
+  return sh;
+}
+
+Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
+  const FastShape sh = bwd_shape(x_dt, W);
   return fast_tiling(B, T, D, sh.cpl, sh.nw, 32, 64, 4096, tune().bwd_rows);
 }
 
@@ -277,7 +290,7 @@ size_t ccv1d_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t dim, int
   if (B <= 0 || T <= 0 || D <= 0 || W < 2 || !valid_dt(x_dtype)) return 0;
   int64_t rows = B * generic_tiling(T).nT;
   if (W <= kMaxFastW && x_dtype != CCV1D_F64) {
-    const int64_t fr = B * bwd_fast_tiling(B, T, D, x_dtype).nTB;
+    const int64_t fr = B * bwd_fast_tiling(B, T, D, W, x_dtype).nTB;
     if (fr > rows) rows = fr;
   }
   return (size_t)(rows * (W + 1) * D * (int64_t)sizeof(float));
@@ -308,7 +321,7 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
     return fail(CCV1D_ERR_INVALID, "cannot take final-state gradients if seq_idx is given");
   if (D == 0) return CCV1D_OK;
   const bool empty = B == 0 || T == 0;
-  const int bcpl = shape_of<BwdCfg>(x_dtype).cpl;
+  const int bcpl = bwd_shape(x_dtype, W).cpl;
   const bool fast = !empty && fast_dtype(x_dtype, W) &&
                     rows_ok(x_dtype, bcpl, T, D, x, x_stride_b, x_stride_t) &&
                     rows_ok(x_dtype, bcpl, T, D, dout, dout_stride_b, dout_stride_t) &&
@@ -319,7 +332,7 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   int64_t rows = 0;
   if (!empty) {
     if (fast) {
-      tl = bwd_fast_tiling(B, T, D, x_dtype);
+      tl = bwd_fast_tiling(B, T, D, W, x_dtype);
       rows = B * tl.nTB;
     } else {
       if (W > kMaxGenericW) return fail(CCV1D_ERR_UNSUPPORTED, "width > %d", kMaxGenericW);

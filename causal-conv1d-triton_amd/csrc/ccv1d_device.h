@@ -93,16 +93,19 @@ __device__ __forceinline__ void st_any(void* p, int64_t i, int dt, float v) {
 
 // ---------------------------------------------------------------------------------------------
 // Channel vectors of the x dtype. One lane moves CPL consecutive channels of one row with a single
-// 8- or 16-byte load or store, so a wave covers 64 * CPL channels (512 B or 1 KiB) per instruction.
+// 4-, 8- or 16-byte load or store, so a wave covers 64 * CPL channels (256 B to 1 KiB) per
+// instruction.
 // ---------------------------------------------------------------------------------------------
 
 typedef float f2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf2v __attribute__((ext_vector_type(2)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x1 __attribute__((ext_vector_type(1)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int BYTES> struct RawOf;
+template <> struct RawOf<4> { using type = u32x1; };
 template <> struct RawOf<8> { using type = u32x2; };
 template <> struct RawOf<16> { using type = u32x4; };
 
@@ -194,8 +197,10 @@ struct RowBuf {
   __device__ __forceinline__ raw ld(int row) const {
     if constexpr (IO::BYTES == 16)
       return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, (uint32_t)row * row_bytes, LD));
-    else
+    else if constexpr (IO::BYTES == 8)
       return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b64(rs, lane_off, (uint32_t)row * row_bytes, LD));
+    else
+      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b32(rs, lane_off, (uint32_t)row * row_bytes, LD));
   }
   __device__ __forceinline__ void st(int row, raw v) const {
     if constexpr (IO::BYTES == 16) {
@@ -203,8 +208,11 @@ struct RowBuf {
                                     (uint64_t)((uint32_t)row * row_bytes + lane_off));
       if (ST == kCacheNT) IO::st_nt(p, v);
       else IO::st(p, v);
-    } else {
+    } else if constexpr (IO::BYTES == 8) {
       __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), rs, lane_off,
+                                            (uint32_t)row * row_bytes, ST);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rs, lane_off,
                                             (uint32_t)row * row_bytes, ST);
     }
   }

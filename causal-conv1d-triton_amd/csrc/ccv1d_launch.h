@@ -26,6 +26,11 @@ template <typename TX> struct FwdCfg {
 };
 template <typename TX> struct BwdCfg {
   static constexpr int CPL = 4;
+  // Widths from kBwdWideW up keep 2 channels per lane: 4 would need about 150-190 VGPRs (the
+  // weights, the x and g windows and the dweight sums are all per channel), one workgroup per CU;
+  // with 2 the kernel holds 4 waves per SIMD (B=4 T=16384 D=4096 W=7 with seq_idx: 657 -> 582 us
+  // per step; at W=4 the benchmark shape is 2.5 us faster with 4 channels).
+  static constexpr int CPL_WIDE = 2;
   static constexpr int NW = 8;
   static constexpr int R = 4;
   static constexpr int XLD = kCacheNT;
@@ -33,6 +38,7 @@ template <typename TX> struct BwdCfg {
   static constexpr int DXST = sizeof(TX) == 2 ? kCacheSC1NT : kCacheNT;
 };
 constexpr int kMaxFastW = 8;     // widths 2..kMaxFastW have register-window kernels
+constexpr int kBwdWideW = 6;     // first width whose backward uses BwdCfg::CPL_WIDE
 constexpr int kMaxGenericW = 128;  // LDS ring of the generic backward: 2 * W * 64 * 4 bytes
 constexpr int kReduceNW = 16;    // waves per reduction workgroup
 constexpr int kGenericL = 64;    // rows per tile of the generic kernels
@@ -69,8 +75,15 @@ static hipError_t fwd_one(const FwdParams& p, hipStream_t s) {
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
 }
 
+// Channels per lane of the backward for width W.
+template <typename TX, int W>
+constexpr int bwd_cpl() {
+  return W >= kBwdWideW ? BwdCfg<TX>::CPL_WIDE : BwdCfg<TX>::CPL;
+}
+
 // The backward's batch depth: C::R rows where the register budget of 4 waves per SIMD holds it
-// (8-byte rows, width <= 4), else 2 rows, which keeps the wider and fp32 instances from spilling.
+// (rows of at most 8 bytes, width <= 4), else 2 rows, which keeps the wider and fp32 instances
+// from spilling.
 template <typename TX, int W>
 constexpr int bwd_rows() {
   using C = BwdCfg<TX>;
@@ -81,8 +94,8 @@ template <typename TX, int W, bool SILU, bool SEQ>
 static hipError_t bwd_one(const BwdParams& p, hipStream_t s) {
   using C = BwdCfg<TX>;
   return launch(reinterpret_cast<const void*>(
-                    &bwd_fast_kernel<TX, W, SILU, SEQ, C::CPL, C::NW, bwd_rows<TX, W>(), C::XLD,
-                                     C::YLD, C::DXST>),
+                    &bwd_fast_kernel<TX, W, SILU, SEQ, bwd_cpl<TX, W>(), C::NW, bwd_rows<TX, W>(),
+                                     C::XLD, C::YLD, C::DXST>),
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
 }
 
