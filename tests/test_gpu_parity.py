@@ -181,7 +181,7 @@ def test_readme_example():
     compare(gpu, oracle_ref(inp, True), True)
 
 
-@pytest.mark.parametrize("W", [2, 3, 4, 5, 7, 9])
+@pytest.mark.parametrize("W", [2, 3, 4, 5, 6, 7, 8, 9])
 @pytest.mark.parametrize("act", [None, "silu"])
 def test_widths_and_lengths(W, act):
     P = W - 1
@@ -197,6 +197,18 @@ def test_widths_and_lengths(W, act):
 @pytest.mark.parametrize("D", [1, 7, 1000, 5376])
 def test_channel_counts(D):
     inp = make_inputs(D, 2, 300, D, 4, init=True)
+    gpu = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=True)
+    compare(gpu, oracle_ref(inp, True, final=True, dfinal=True, need_dinit=True), True)
+
+
+@pytest.mark.parametrize("W", [6, 8])
+@pytest.mark.parametrize("D", [1002, 260])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+def test_wide_widths_channel_counts(W, D, xdt):
+    """Widths from 6 keep 2 channels per lane in the backward: D = 1002 (not a multiple of 4, so
+    the forward takes the generic kernel while the backward stays vectorised) and D = 260 (a last
+    wave column that is mostly empty)."""
+    inp = make_inputs(W * 10 + D, 3, 333, D, W, xdt=xdt, init=True)
     gpu = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=True)
     compare(gpu, oracle_ref(inp, True, final=True, dfinal=True, need_dinit=True), True)
 
@@ -253,8 +265,23 @@ def test_seq_idx(W, init):
     assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0)
 
 
-def test_seq_idx_int64_and_all_equal():
-    B, T, D, W = 2, 300, 128, 4
+@pytest.mark.parametrize("W", [4, 7])
+def test_seq_idx_long_segments(W):
+    """Long segments with few boundaries: most tiles lie inside one segment (and run the seq-free
+    code), the others carry a boundary or padding; both kinds must match the oracle, and padding
+    positions stay exactly zero."""
+    B, T, D = 2, 4096, 512
+    seq = varlen_seq(40 + W, B, T, lo=300, hi=1500, pad_frac=0.03)
+    inp = make_inputs(50 + W, B, T, D, W, init=True, seq=seq)
+    gpu = run_gpu(inp, "silu", init_grad=True)
+    compare(gpu, oracle_ref(inp, True, need_dinit=True), True)
+    pad = seq < 0
+    assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0)
+
+
+@pytest.mark.parametrize("W", [4, 7])
+def test_seq_idx_int64_and_all_equal(W):
+    B, T, D = 2, 300, 128
     inp = make_inputs(3, B, T, D, W, init=True)
     base = run_gpu(inp, "silu", init_grad=True)
     inp_eq = dict(inp, seq=torch.full((B, T), 5, dtype=torch.int64))
