@@ -50,8 +50,13 @@ FastShape shape_of(int x_dt) {
   }
 }
 
+// Longest tile of the vectorised kernels (defaults and overrides alike). With seq_idx a wave reads the
+// ids of its tile and both halos (L + 2 (W - 1) rows) up front into one RowIds.
+constexpr int kMaxTileRows = 64;
+static_assert(kMaxTileRows + 2 * (kMaxFastW - 1) <= kRowIds, "tile and halos must fit one RowIds");
+
 // Row tiling overrides for tuning sweeps, read once: CCV1D_FWD_ROWS / CCV1D_BWD_ROWS (rows per tile
-// of the vectorised kernels; a power of two in [8, 1024]).
+// of the vectorised kernels; a power of two in [8, kMaxTileRows]).
 struct Tune {
   int fwd_rows = 0;
   int bwd_rows = 0;
@@ -64,7 +69,7 @@ const Tune& tune() {
       const char* e = std::getenv(name);
       if (!e) return 0;
       const int r = std::atoi(e);
-      return (r >= 8 && r <= 1024 && (r & (r - 1)) == 0) ? r : 0;
+      return (r >= 8 && r <= kMaxTileRows && (r & (r - 1)) == 0) ? r : 0;
     };
     v.fwd_rows = rd("CCV1D_FWD_ROWS");
     v.bwd_rows = rd("CCV1D_BWD_ROWS");
@@ -111,7 +116,7 @@ constexpr int64_t kFwdSmallGrid = 256;
 
 Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
   const FastShape sh = shape_of<FwdCfg>(x_dt);
-  Tiling t = fast_tiling(B, T, D, sh.cpl, sh.nw, 16, 64, 4096, tune().fwd_rows);
+  Tiling t = fast_tiling(B, T, D, sh.cpl, sh.nw, 16, kMaxTileRows, 4096, tune().fwd_rows);
   if (tune().fwd_rows == 0 && t.L == 16 && t.nBlk < kFwdSmallGrid)
     t = fast_tiling(B, T, D, sh.cpl, sh.nw, 8, 8, 4096, 8);
   return t;
@@ -132,7 +137,7 @@ FastShape bwd_shape(int x_dt, int64_t W) {
 
 Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
   const FastShape sh = bwd_shape(x_dt, W);
-  return fast_tiling(B, T, D, sh.cpl, sh.nw, 32, 64, 4096, tune().bwd_rows);
+  return fast_tiling(B, T, D, sh.cpl, sh.nw, 32, kMaxTileRows, 4096, tune().bwd_rows);
 }
 
 Tiling generic_tiling(int64_t T) {

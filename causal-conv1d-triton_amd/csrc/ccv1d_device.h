@@ -291,6 +291,10 @@ __device__ __forceinline__ float dsilu_times(float dy, float z) {
   return dy * s * fmaf(z, 1.0f - s, 1.0f);
 }
 
+// Rows whose sequence ids a wave of the vectorised kernels reads up front (RowIds): its tile and both
+// halos must fit.
+constexpr int kRowIds = 128;
+
 // Sequence id of row t of concat(initial_states, x) (causal_conv1d.py:17-25): rows t < 0 belong to
 // seq_idx[b, 0] when there are initial states and are -1 otherwise; rows t >= T are -1.
 __device__ __forceinline__ int32_t seq_at(const int32_t* seqb, int t, int T, bool has_init) {

@@ -103,22 +103,42 @@ struct TileCoord {
   }
 };
 
-// True when rows r0 .. r1-1 of concat(initial_states, x) all carry one sequence id and it is not
-// padding (>= 0). Every sequence mask of such a tile is 1 and no row of it is zeroed, so the tile can
-// run the kernels' seq_idx-free code, which then gives bit-identical results. Lane j reads the ids
-// of rows r0 + j, r0 + j + 64, ...; the wave vote needs every lane of the wave active.
-__device__ __forceinline__ bool rows_in_one_segment(const int32_t* sb, int r0, int r1, int T,
-                                                    bool has_init) {
-  const int lane = threadIdx.x & 63;
-  const int32_t id0 = __builtin_amdgcn_readfirstlane(seq_at(sb, r0, T, has_init));
-  bool ok = id0 >= 0;
-  for (int base = r0; base < r1; base += 64) {
-    const int r = base + lane;
-    const int32_t v = r < r1 ? seq_at(sb, r, T, has_init) : id0;
-    ok = __all(v == id0) && ok;
+// Sequence ids of rows r0 .. r0 + 127 of concat(initial_states, x) (kRowIds rows), row r0 + j in
+// lane j of `lo` (j < 64) or lane j - 64 of `hi`, read with two vector loads issued together. A tile
+// and both its halos span at most 64 + 2 * 7 rows, so one RowIds serves every row a tile touches:
+// at() gives the id of a row to the whole wave (v_readlane) without a load of its own, and no load
+// of ids then sits in the tile's pipelined loop, where its wait would also cover the loads and
+// stores issued before it.
+static_assert(kRowIds == 128, "RowIds holds two 64-lane vectors");
+struct RowIds {
+  int32_t lo = 0, hi = 0;
+  int r0 = 0;
+  RowIds() = default;
+  __device__ __forceinline__ RowIds(const int32_t* sb, int first, int T, bool has_init) : r0(first) {
+    const int lane = threadIdx.x & 63;
+    lo = seq_at(sb, r0 + lane, T, has_init);
+    hi = seq_at(sb, r0 + 64 + lane, T, has_init);
   }
-  return ok;
-}
+  // Id of row `row`, r0 <= row < r0 + kRowIds, row wave-uniform.
+  __device__ __forceinline__ int32_t at(int row) const {
+    const int j = row - r0;
+    const int32_t a = __builtin_amdgcn_readlane(lo, j & 63);
+    const int32_t b = __builtin_amdgcn_readlane(hi, j & 63);
+    return j < 64 ? a : b;
+  }
+  // True when rows r0 .. r1-1 (r0 < r1 <= r0 + kRowIds) all carry one sequence id and it is not
+  // padding (>= 0). Every sequence mask of such a tile is 1 and no row of it is zeroed, so the tile
+  // can run the kernels' seq_idx-free code, which then gives bit-identical results. The wave votes
+  // need every lane of the wave active.
+  __device__ __forceinline__ bool one_segment(int r1) const {
+    const int lane = threadIdx.x & 63;
+    const int32_t id0 = __builtin_amdgcn_readlane(lo, 0);
+    bool ok = id0 >= 0;
+    ok = __all((r0 + lane < r1 ? lo : id0) == id0) && ok;
+    ok = __all((r0 + 64 + lane < r1 ? hi : id0) == id0) && ok;
+    return ok;
+  }
+};
 
 // =============================================================================================
 // Forward: out = act(conv(x)) and final_states (causal_conv1d.py:44-164).
@@ -316,7 +336,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
   const int t1 = min(t0 + p.tl.L, T);
   const int32_t* __restrict__ sb = SEQ ? p.seq + (int64_t)tc.b * T : nullptr;
   // A tile inside one segment runs the seq_idx-free code (decided before any lane leaves).
-  const bool masked = SEQ && !rows_in_one_segment(sb, t0 - P, t1, T, p.has_init);
+  const bool masked = SEQ && !RowIds(sb, t0 - P, T, p.has_init).one_segment(t1);
   const int grp = tc.gw * 64 + lane;
   if (grp >= p.D / CPL) return;
   const int c0 = grp * CPL;
@@ -471,7 +491,7 @@ constexpr int bwd_lds_floats() {
 
 // One wave's tile of the backward (the whole kernel but the choice of SEQ, see bwd_fast_kernel).
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int YLD, int DXST>
-__device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds) {
+__device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const RowIds& ids) {
   using IO = VecIO<TX, CPL>;
   using raw = typename IO::raw;
   constexpr int P = W - 1;
@@ -496,7 +516,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds) {
   const int t_main = min(t0 + P, t_end);
   const int emit_lo = (tile == 0 && p.need_dinit) ? -P : t0;
   const int64_t state_off = (int64_t)tc.b * P * D + c0;
-  const int32_t* __restrict__ sb = SEQ ? p.seq + (int64_t)tc.b * T : nullptr;
+  // Sequence ids (SEQ): `ids` holds rows t0-P .. t0-P+127, which cover the tile and both halos.
   const TX* dfb = p.has_dfinal ? static_cast<const TX*>(p.dfin) + state_off : nullptr;
   const RowBuf<TX, CPL, XLD> X(static_cast<const TX*>(p.x) + (int64_t)tc.b * p.s_xb, p.x_bytes, c0, p.s_xt);
   const RowBuf<TX, CPL, YLD> Y(static_cast<const TX*>(p.dy) + (int64_t)tc.b * p.s_yb, p.y_bytes, c0, p.s_yt);
@@ -528,8 +548,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds) {
   };
 
   raw Ax[R], Ay[R], Bx[R], By[R];
-  int32_t As[R], Bs[R];
-  auto load = [&](raw (&bx)[R], raw (&by)[R], int32_t (&bs)[R], int t) {
+  auto load = [&](raw (&bx)[R], raw (&by)[R], int t) {
     // Rows past the end are clamped to the last row: a duplicate read keeps the number of loads in
     // flight fixed, so the compiler's wait counts stay exact.
 #pragma unroll
@@ -538,8 +557,6 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds) {
       bx[r] = X.ld(row);
       by[r] = Y.ld(row);
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r) bs[r] = SEQ ? sb[min(t + r, t_end - 1)] : 0;
   };
 
   float* halo_out = lds + wave * P * COLS + lane * CPL;
@@ -558,7 +575,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds) {
       px[q] = X.ld(row);
       py[q] = Y.ld(row);
     }
-    load(Ax, Ay, As, t_main);
+    load(Ax, Ay, t_main);
     load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
 #pragma unroll
     for (int k = 0; k < P; ++k) {
@@ -570,7 +587,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds) {
 #pragma unroll
         for (int i = 0; i < CPL; ++i) s.xw[k][i] = 0.0f;
       }
-      s.sw[k] = SEQ ? seq_at(sb, row, T, has_init) : 0;
+      s.sw[k] = SEQ ? ids.at(row) : 0;
 #pragma unroll
       for (int i = 0; i < CPL; ++i) s.gw[k][i] = 0.0f;
     }
@@ -581,7 +598,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds) {
       const int t = t0 + q;
       if (t < t_main) {
         float dx[CPL];
-        s.step(t, px[q], py[q], SEQ ? sb[t] : 0, dx);
+        s.step(t, px[q], py[q], SEQ ? ids.at(t) : 0, dx);
         emit_any(t - P, dx);
       }
 #pragma unroll
@@ -592,28 +609,28 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds) {
 
   if (active) {
     // Steady state: every step stores dx of row t - P, with t0 <= t - P < T - P.
-    auto compute = [&](const raw (&bx)[R], const raw (&by)[R], const int32_t (&bs)[R], int t) {
+    auto compute = [&](const raw (&bx)[R], const raw (&by)[R], int t) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float dx[CPL];
-        s.step(t + r, bx[r], by[r], bs[r], dx);
+        s.step(t + r, bx[r], by[r], SEQ ? ids.at(t + r) : 0, dx);
         DX.st(t + r - P, IO::pack(dx));
       }
     };
     int t = t_main;
     for (; t + 2 * R <= t_end; t += 2 * R) {
-      load(Bx, By, Bs, t + R);
-      compute(Ax, Ay, As, t);
-      load(Ax, Ay, As, t + 2 * R);
-      compute(Bx, By, Bs, t + R);
+      load(Bx, By, t + R);
+      compute(Ax, Ay, t);
+      load(Ax, Ay, t + 2 * R);
+      compute(Bx, By, t + R);
     }
     if (t + R <= t_end) {
-      compute(Ax, Ay, As, t);
+      compute(Ax, Ay, t);
       t += R;
     }
     for (; t < t_end; ++t) {
       float dx[CPL];
-      s.step(t, X.ld(t), Y.ld(t), SEQ ? sb[t] : 0, dx);
+      s.step(t, X.ld(t), Y.ld(t), SEQ ? ids.at(t) : 0, dx);
       emit_any(t - P, dx);
     }
 
@@ -626,7 +643,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds) {
         float g[CPL], dx[CPL];
 #pragma unroll
         for (int i = 0; i < CPL; ++i) g[i] = halo_in[q * COLS + i];
-        const int32_t st = SEQ ? seq_at(sb, tt, T, has_init) : 0;
+        const int32_t st = SEQ ? ids.at(tt) : 0;
         s.dx_row(g, st, true, dx);
         emit_any(tt - P, dx);
         shift_in(s.gw, g);
@@ -691,7 +708,8 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds) {
 
 // A wave whose tile (its rows and both halos, t0-P .. own_end+P-1) lies inside one non-padding
 // segment runs the seq_idx-free instantiation of bwd_tile; the others run the masked one. Both have
-// the same LDS barriers, so the waves of one workgroup may take different ones.
+// the same LDS barriers, so the waves of one workgroup may take different ones. The host keeps
+// tiles short enough (L + 2 (W - 1) <= kRowIds) for one RowIds to cover a tile and its halos.
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int YLD, int DXST>
 __global__ __launch_bounds__(NW * 64, (bwd_waves_per_simd<TX, W, CPL>())) void bwd_fast_kernel(
     const BwdParams p) {
@@ -702,13 +720,18 @@ __global__ __launch_bounds__(NW * 64, (bwd_waves_per_simd<TX, W, CPL>())) void b
     const int tile = tc.tb * NW + wave;
     const int t0 = tile * p.tl.L;
     const int r1 = min(t0 + p.tl.L + W - 1, p.T);
-    if (tile < p.tl.nT &&
-        rows_in_one_segment(p.seq + (int64_t)tc.b * p.T, t0 - (W - 1), r1, p.T, p.has_init)) {
-      bwd_tile<TX, W, SILU, false, CPL, NW, R, XLD, YLD, DXST>(p, lds);
+    const RowIds ids(p.seq + (int64_t)tc.b * p.T, t0 - (W - 1), p.T, p.has_init);
+    // Evaluated on every path (its result is unused past the last tile), so that both id vectors
+    // have arrived before either instantiation starts and no wait for them is left to its loop.
+    const bool one = ids.one_segment(r1);
+    if (tile < p.tl.nT && one) {
+      bwd_tile<TX, W, SILU, false, CPL, NW, R, XLD, YLD, DXST>(p, lds, ids);
       return;
     }
+    bwd_tile<TX, W, SILU, SEQ, CPL, NW, R, XLD, YLD, DXST>(p, lds, ids);
+  } else {
+    bwd_tile<TX, W, SILU, false, CPL, NW, R, XLD, YLD, DXST>(p, lds, RowIds());
   }
-  bwd_tile<TX, W, SILU, SEQ, CPL, NW, R, XLD, YLD, DXST>(p, lds);
 }
 
 }  // namespace ccv1d
