@@ -52,8 +52,12 @@ FastShape shape_of(int x_dt) {
 
 // Longest tile of the vectorised kernels (defaults and overrides alike). With seq_idx a wave reads the
 // ids of its tile and both halos (L + 2 (W - 1) rows) up front into one RowIds.
+// Every tile is at least kMinTileRows long (defaults and overrides), longer than any window (W - 1),
+// so only the first tile of a row has a window outside x.
 constexpr int kMaxTileRows = 64;
+constexpr int kMinTileRows = 8;
 static_assert(kMaxTileRows + 2 * (kMaxFastW - 1) <= kRowIds, "tile and halos must fit one RowIds");
+static_assert(kMinTileRows > kMaxFastW - 1, "a tile must be longer than the window");
 
 // Row tiling overrides for tuning sweeps, read once: CCV1D_FWD_ROWS / CCV1D_BWD_ROWS (rows per tile
 // of the vectorised kernels; a power of two in [8, kMaxTileRows]).
@@ -69,7 +73,7 @@ const Tune& tune() {
       const char* e = std::getenv(name);
       if (!e) return 0;
       const int r = std::atoi(e);
-      return (r >= 8 && r <= kMaxTileRows && (r & (r - 1)) == 0) ? r : 0;
+      return (r >= kMinTileRows && r <= kMaxTileRows && (r & (r - 1)) == 0) ? r : 0;
     };
     v.fwd_rows = rd("CCV1D_FWD_ROWS");
     v.bwd_rows = rd("CCV1D_BWD_ROWS");
@@ -118,7 +122,7 @@ Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
   const FastShape sh = shape_of<FwdCfg>(x_dt);
   Tiling t = fast_tiling(B, T, D, sh.cpl, sh.nw, 16, kMaxTileRows, 4096, tune().fwd_rows);
   if (tune().fwd_rows == 0 && t.L == 16 && t.nBlk < kFwdSmallGrid)
-    t = fast_tiling(B, T, D, sh.cpl, sh.nw, 8, 8, 4096, 8);
+    t = fast_tiling(B, T, D, sh.cpl, sh.nw, kMinTileRows, kMinTileRows, 4096, kMinTileRows);
   return t;
 }
 

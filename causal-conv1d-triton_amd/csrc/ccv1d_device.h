@@ -246,6 +246,43 @@ __device__ __forceinline__ void ld_vec_any(const void* p, int64_t off, int dt, f
   }
 }
 
+// M rows of N consecutive elements, `stride` elements apart, converted to fp32. One dtype switch
+// for all rows, so the M * N loads issue before any of them is waited for.
+template <int M, int N>
+__device__ __forceinline__ void ld_rows_any(const void* p, int64_t off, int64_t stride, int dt,
+                                            float (&f)[M][N]) {
+  switch (dt) {
+    case DT_F32: {
+      const float* q = static_cast<const float*>(p) + off;
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < N; ++i) f[m][i] = q[m * stride + i];
+    } break;
+    case DT_F16: {
+      const _Float16* q = static_cast<const _Float16*>(p) + off;
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < N; ++i) f[m][i] = static_cast<float>(q[m * stride + i]);
+    } break;
+    case DT_BF16: {
+      const __bf16* q = static_cast<const __bf16*>(p) + off;
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < N; ++i) f[m][i] = static_cast<float>(q[m * stride + i]);
+    } break;
+    default: {
+      const double* q = static_cast<const double*>(p) + off;
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < N; ++i) f[m][i] = static_cast<float>(q[m * stride + i]);
+    } break;
+  }
+}
+
 template <int N>
 __device__ __forceinline__ void st_vec_any(void* p, int64_t off, int dt, const float (&f)[N]) {
   switch (dt) {

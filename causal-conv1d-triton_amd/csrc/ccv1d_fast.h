@@ -208,12 +208,12 @@ struct FwdLaneRev {
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int R, int XLD, int OST>
 __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBuf<TX, CPL, XLD>& X,
                                                  const RowBuf<TX, CPL, kCachePlain, OST>& O,
-                                                 const int32_t* __restrict__ sb, int c0, int t0,
-                                                 int t1, int64_t init_off) {
+                                                 const RowIds& ids, int c0, int t0, int t1,
+                                                 int64_t init_off, TX* fin) {
   using IO = VecIO<TX, CPL>;
   using raw = typename IO::raw;
   constexpr int P = W - 1;
-  const int T = p.T, D = p.D;
+  const int D = p.D;
   const bool halo_in_x = t0 >= P;
   raw hr[P];
   if (halo_in_x) {
@@ -226,26 +226,27 @@ __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBu
 #pragma unroll
     for (int r = 0; r < R; ++r) buf[r] = X.ld(min(t + r, t1 - 1));
 #pragma unroll
-    for (int r = 0; r < R; ++r) sq[r] = SEQ ? sb[min(t + r, t1 - 1)] : 0;
+    for (int r = 0; r < R; ++r) sq[r] = SEQ ? ids.at(min(t + r, t1 - 1)) : 0;
   };
   load(A, sA, t0);
 
   FwdLane<TX, W, SILU, SEQ, CPL> s;
   load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
+  // Tiles are at least 8 rows long, so a tile starts at row 0 or at a row >= 8 > P: a window not in
+  // x is the first tile's, the P initial-state rows (or zeros).
+  if (halo_in_x) {
 #pragma unroll
-  for (int k = 0; k < P; ++k) {
-    if (halo_in_x) IO::unpack(hr[k], s.xw[k]);
-    else {
-      const int row = t0 - P + k;
-      if (row >= 0) IO::unpack(X.ld(row), s.xw[k]);
-      else if (p.has_init) ld_vec_any<CPL>(p.init, init_off + (int64_t)(row + P) * D, p.i_dt, s.xw[k]);
-      else {
+    for (int k = 0; k < P; ++k) IO::unpack(hr[k], s.xw[k]);
+  } else if (p.has_init) {
+    ld_rows_any<P, CPL>(p.init, init_off, D, p.i_dt, s.xw);
+  } else {
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) s.xw[k][i] = 0.0f;
-      }
-    }
-    s.sw[k] = SEQ ? seq_at(sb, t0 - P + k, T, p.has_init) : 0;
+    for (int k = 0; k < P; ++k)
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) s.xw[k][i] = 0.0f;
   }
+#pragma unroll
+  for (int k = 0; k < P; ++k) s.sw[k] = SEQ ? ids.at(t0 - P + k) : 0;
 
   auto compute = [&](const raw (&buf)[R], const int32_t (&sq)[R], int t) {
 #pragma unroll
@@ -262,7 +263,13 @@ __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBu
     compute(A, sA, t);
     t += R;
   }
-  for (; t < t1; ++t) O.st(t, s.row(X.ld(t), SEQ ? sb[t] : 0));
+  for (; t < t1; ++t) O.st(t, s.row(X.ld(t), SEQ ? ids.at(t) : 0));
+  // final_states of the tile ending at T: the window now holds rows T-P .. T-1 of
+  // concat(initial_states, x) in fp32, exact copies of x.dtype values or converted initial states.
+  if (fin) {
+#pragma unroll
+    for (int k = 0; k < P; ++k) IO::st(fin + (int64_t)k * D, IO::pack(s.xw[k]));
+  }
 }
 
 // One tile walked backward (outputs t1-1 down to t0), for tiles with t0 >= 8 > P, whose rows all
@@ -271,8 +278,8 @@ __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBu
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int R, int XLD, int OST>
 __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBuf<TX, CPL, XLD>& X,
                                                  const RowBuf<TX, CPL, kCachePlain, OST>& O,
-                                                 const int32_t* __restrict__ sb, int c0, int t0,
-                                                 int t1) {
+                                                 const RowIds& ids, int c0, int t0, int t1,
+                                                 TX* fin) {
   using IO = VecIO<TX, CPL>;
   using raw = typename IO::raw;
   constexpr int P = W - 1;
@@ -280,13 +287,18 @@ __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBu
   raw wr[P + 1];
 #pragma unroll
   for (int k = 0; k <= P; ++k) wr[k] = X.ld(t1 - 1 - P + k);
+  // final_states of the tile ending at T: rows T-P .. T-1, all in x here, are wr[1..P].
+  if (fin) {
+#pragma unroll
+    for (int k = 0; k < P; ++k) IO::st(fin + (int64_t)k * p.D, wr[k + 1]);
+  }
   raw A[R], B[R];
   int32_t sA[R], sB[R];
   auto load = [&](raw (&buf)[R], int32_t (&sq)[R], int row) {
 #pragma unroll
     for (int r = 0; r < R; ++r) buf[r] = X.ld(max(row - r, lo));
 #pragma unroll
-    for (int r = 0; r < R; ++r) sq[r] = SEQ ? sb[max(row - r, lo)] : 0;
+    for (int r = 0; r < R; ++r) sq[r] = SEQ ? ids.at(max(row - r, lo)) : 0;
   };
   load(A, sA, t1 - 2 - P);
 
@@ -295,7 +307,7 @@ __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBu
 #pragma unroll
   for (int k = 0; k <= P; ++k) {
     IO::unpack(wr[k], s.xv[k]);
-    s.sv[k] = SEQ ? sb[t1 - 1 - P + k] : 0;
+    s.sv[k] = SEQ ? ids.at(t1 - 1 - P + k) : 0;
   }
 
   auto compute = [&](const raw (&buf)[R], const int32_t (&sq)[R], int t) {
@@ -315,7 +327,7 @@ __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBu
   }
   for (; t >= t0; --t) {
     const int row = max(t - P - 1, lo);
-    O.st(t, s.row(X.ld(row), SEQ ? sb[row] : 0));
+    O.st(t, s.row(X.ld(row), SEQ ? ids.at(row) : 0));
   }
 }
 
@@ -324,7 +336,6 @@ __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBu
 // start, or both at their end), so the second read finds them in L2 instead of memory.
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int OST>
 __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
-  using IO = VecIO<TX, CPL>;
   constexpr int P = W - 1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -334,9 +345,10 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
   const int T = p.T, D = p.D;
   const int t0 = tile * p.tl.L;
   const int t1 = min(t0 + p.tl.L, T);
-  const int32_t* __restrict__ sb = SEQ ? p.seq + (int64_t)tc.b * T : nullptr;
-  // A tile inside one segment runs the seq_idx-free code (decided before any lane leaves).
-  const bool masked = SEQ && !RowIds(sb, t0 - P, T, p.has_init).one_segment(t1);
+  // Ids of rows t0-P .. t0-P+127, which cover the tile and its halo (SEQ). A tile inside one segment
+  // runs the seq_idx-free code (decided before any lane leaves).
+  const RowIds ids = SEQ ? RowIds(p.seq + (int64_t)tc.b * T, t0 - P, T, p.has_init) : RowIds();
+  const bool masked = SEQ && !ids.one_segment(t1);
   const int grp = tc.gw * 64 + lane;
   if (grp >= p.D / CPL) return;
   const int c0 = grp * CPL;
@@ -346,30 +358,15 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
   const RowBuf<TX, CPL, kCachePlain, OST> O(static_cast<const TX*>(p.out) + (int64_t)tc.b * T * D,
                                             p.o_bytes, c0, D);
   const int64_t init_off = (int64_t)tc.b * P * D + c0;
+  // final_states (causal_conv1d.py:153-164) come from the registers of the tile ending at T.
+  TX* const fin = (p.has_final && t1 == T) ? static_cast<TX*>(p.fin) + init_off : nullptr;
 
   if (masked) {
-    if (tile & 1) fwd_tile_reverse<TX, W, SILU, SEQ, CPL, R>(p, X, O, sb, c0, t0, t1);
-    else fwd_tile_forward<TX, W, SILU, SEQ, CPL, R>(p, X, O, sb, c0, t0, t1, init_off);
+    if (tile & 1) fwd_tile_reverse<TX, W, SILU, SEQ, CPL, R>(p, X, O, ids, c0, t0, t1, fin);
+    else fwd_tile_forward<TX, W, SILU, SEQ, CPL, R>(p, X, O, ids, c0, t0, t1, init_off, fin);
   } else {
-    if (tile & 1) fwd_tile_reverse<TX, W, SILU, false, CPL, R>(p, X, O, sb, c0, t0, t1);
-    else fwd_tile_forward<TX, W, SILU, false, CPL, R>(p, X, O, sb, c0, t0, t1, init_off);
-  }
-
-  // final_states = rows T-P .. T-1 of concat(initial_states, x) (causal_conv1d.py:153-164).
-  if (p.has_final && t1 == T) {
-    TX* fb = static_cast<TX*>(p.fin) + init_off;
-#pragma unroll
-    for (int q = 0; q < P; ++q) {
-      const int row = T - P + q;
-      float f[CPL];
-      if (row >= 0) IO::unpack(X.ld(row), f);
-      else if (p.has_init) ld_vec_any<CPL>(p.init, init_off + (int64_t)(row + P) * D, p.i_dt, f);
-      else {
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) f[i] = 0.0f;
-      }
-      IO::st(fb + q * D, IO::pack(f));
-    }
+    if (tile & 1) fwd_tile_reverse<TX, W, SILU, false, CPL, R>(p, X, O, ids, c0, t0, t1, fin);
+    else fwd_tile_forward<TX, W, SILU, false, CPL, R>(p, X, O, ids, c0, t0, t1, init_off, fin);
   }
 }
 
@@ -577,17 +574,22 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
     }
     load(Ax, Ay, t_main);
     load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
+    // Tiles are at least 8 rows long, so a tile starts at row 0 or at a row >= 8 > P: a window not
+    // in x is the first tile's, the P initial-state rows (or zeros).
+    if (halo_in_x) {
 #pragma unroll
-    for (int k = 0; k < P; ++k) {
-      const int row = t0 - P + k;
-      if (halo_in_x) IO::unpack(hr[k], s.xw[k]);
-      else if (row >= 0) IO::unpack(X.ld(row), s.xw[k]);
-      else if (has_init) ld_vec_any<CPL>(p.init, state_off + (int64_t)(row + P) * D, p.i_dt, s.xw[k]);
-      else {
+      for (int k = 0; k < P; ++k) IO::unpack(hr[k], s.xw[k]);
+    } else if (has_init) {
+      ld_rows_any<P, CPL>(p.init, state_off, D, p.i_dt, s.xw);
+    } else {
+#pragma unroll
+      for (int k = 0; k < P; ++k)
 #pragma unroll
         for (int i = 0; i < CPL; ++i) s.xw[k][i] = 0.0f;
-      }
-      s.sw[k] = SEQ ? ids.at(row) : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+      s.sw[k] = SEQ ? ids.at(t0 - P + k) : 0;
 #pragma unroll
       for (int i = 0; i < CPL; ++i) s.gw[k][i] = 0.0f;
     }

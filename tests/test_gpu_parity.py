@@ -313,6 +313,35 @@ def test_state_handoff_bit_exact():
         assert f2 is buf and torch.equal(buf, fin) and torch.equal(o2, full)
 
 
+@pytest.mark.parametrize("W", [2, 4, 8])
+@pytest.mark.parametrize("idt", [None, torch.bfloat16, torch.float32])
+def test_final_states_from_either_tile_walk(W, idt):
+    """final_states are written from the registers of the tile that ends at T, which walks forward
+    in time (even tiles) or backward (odd tiles). At D=1024 these lengths end on an even and on an
+    odd tile for each tile length the forward uses (8, 16, 32 and 64 rows), with no initial
+    states, bf16 ones and fp32 ones. Bit-exact: final == cat(initial_states, x)[:, T:], and two
+    chunks with the state handed over give the full pass."""
+    P, D = W - 1, 1024
+    g = torch.Generator(device=DEV).manual_seed(W)
+    w = torch.randn(D, W, generator=g, device=DEV)
+    for B, T in ((1, 16), (1, 24), (8, 904), (8, 920), (8, 4072), (2, 16392), (8, 8136),
+                 (4, 16392)):
+        x = torch.randn(B, T, D, generator=g, device=DEV).to(torch.bfloat16)
+        init = None if idt is None else torch.randn(B, P, D, generator=g, device=DEV).to(idt)
+        with torch.no_grad():
+            out, fin = causal_conv1d_fn(x, w, initial_states=init, return_final_states=True,
+                                        activation="silu")
+            assert torch.equal(fin, x[:, T - P:]), (W, B, T)
+            cut = T // 2 + 1
+            o1, s1 = causal_conv1d_fn(x[:, :cut], w, initial_states=init, return_final_states=True,
+                                      activation="silu")
+            assert torch.equal(s1, x[:, cut - P:cut]), (W, B, T)
+            o2, s2 = causal_conv1d_fn(x[:, cut:], w, initial_states=s1, return_final_states=True,
+                                      activation="silu")
+            assert torch.equal(s2, fin), (W, B, T)
+            assert torch.equal(torch.cat([o1, o2], dim=1), out), (W, B, T)
+
+
 def test_deterministic_weight_grads():
     inp = make_inputs(9, 4, 4096, 1024, 4)
     a = run_gpu(inp, "silu")
