@@ -1,8 +1,13 @@
-"""ctypes binding of libccv1d.so, the C ABI declared in include/ccv1d.h.
+"""Binding of libccv1d.so, the C ABI declared in include/ccv1d.h.
 
 The library is the only compute path: if it is missing or fails to load, every call raises. It must be
 loaded after `import torch` so that it binds to the HIP runtime torch has already loaded (same
 soname), which makes torch's streams and device pointers valid arguments.
+
+The two launch entry points go through the package's CPython extension `_ccv1d_native`
+(csrc/ccv1d_pyext.c) when it is built, which links the same libccv1d.so and converts the arguments
+at a fraction of ctypes' per-call cost; otherwise, and for everything else, through ctypes. Both
+call the same C functions with the same arguments.
 """
 
 import ctypes
@@ -19,6 +24,11 @@ _c_int = ctypes.c_int
 _c_ptr = ctypes.c_void_p
 
 _lib = None
+
+try:
+    from . import _ccv1d_native as _native
+except ImportError:  # not built: the ctypes binding serves every call
+    _native = None
 
 
 class CCV1DError(RuntimeError):
@@ -105,11 +115,10 @@ def _stream(index: int) -> int:
 
 
 def fwd(x, weight, bias, seq_idx, initial_states, out, final_states, silu: bool) -> None:
-    lib = _lib if _lib is not None else load()
     B, T, D = x.shape
     W = weight.shape[1]
     dev = x.get_device()
-    rc = lib.ccv1d_fwd(
+    args = (
         x.data_ptr(), x.stride(0), x.stride(1), _code(x),
         weight.data_ptr(), _code(weight),
         _ptr(bias), 0 if bias is None else _code(bias),
@@ -119,8 +128,12 @@ def fwd(x, weight, bias, seq_idx, initial_states, out, final_states, silu: bool)
         B, T, D, W,
         int(silu), dev, _stream(dev),
     )
+    if _native is not None:
+        rc = _native.fwd(*args)
+    else:
+        rc = (_lib if _lib is not None else load()).ccv1d_fwd(*args)
     if rc:
-        _check(rc, lib)
+        _check(rc, load())
 
 
 def bwd_workspace_bytes(B: int, T: int, D: int, W: int, x_dtype: torch.dtype) -> int:
@@ -129,7 +142,6 @@ def bwd_workspace_bytes(B: int, T: int, D: int, W: int, x_dtype: torch.dtype) ->
 
 def bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit, dweight, dbias,
         workspace, silu: bool) -> None:
-    lib = _lib if _lib is not None else load()
     B, T, D = x.shape
     W = weight.shape[1]
     dev = x.get_device()
@@ -137,7 +149,7 @@ def bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit
         raise TypeError(f"dout dtype {dout.dtype} differs from x dtype {x.dtype}")
     if dfinal_states is not None and dfinal_states.dtype != x.dtype:
         raise TypeError(f"dfinal_states dtype {dfinal_states.dtype} differs from x dtype {x.dtype}")
-    rc = lib.ccv1d_bwd(
+    args = (
         x.data_ptr(), x.stride(0), x.stride(1), _code(x),
         weight.data_ptr(), _code(weight),
         _ptr(bias), 0 if bias is None else _code(bias),
@@ -150,5 +162,9 @@ def bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit
         B, T, D, W,
         int(silu), dev, _stream(dev),
     )
+    if _native is not None:
+        rc = _native.bwd(*args)
+    else:
+        rc = (_lib if _lib is not None else load()).ccv1d_bwd(*args)
     if rc:
-        _check(rc, lib)
+        _check(rc, load())

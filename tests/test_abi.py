@@ -110,3 +110,66 @@ def test_bwd_rejects_invalid_arguments(kw, code, msg):
     lib = _ffi.load()
     assert _bwd(lib, **kw) == code
     assert msg in lib.ccv1d_last_error().decode()
+
+
+# The package's CPython binding of the two launch entry points (csrc/ccv1d_pyext.c): same C
+# functions, same arguments, same status codes, and one library instance shared with ctypes (so
+# ccv1d_last_error reads the error of a call made through either).
+
+def _native():
+    assert _ffi._native is not None, "the CPython binding is built with the library (make)"
+    return _ffi._native
+
+
+def test_native_binding_matches_the_library():
+    nat = _native()
+    assert nat.abi_version() == _ffi.load().ccv1d_abi_version()
+    libs = {line.split()[-1] for line in open("/proc/self/maps") if "libccv1d" in line}
+    assert libs == {os.path.realpath(_ffi.library_path())}
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(W=1), "width"),
+    (dict(xdt=7), "dtype"),
+    (dict(out=None), "out is null"),
+    (dict(seq=1 << 23, fin=1 << 24), "final states"),
+])
+def test_native_fwd_rejects_invalid_arguments(kw, msg):
+    lib = _ffi.load()
+    assert _fwd(_NativeAsLib(), **kw) == 1
+    assert msg in lib.ccv1d_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(db=1 << 25), 1, "dbias"),
+    (dict(ws=None, wsb=0), 3, "workspace"),
+    (dict(W=200, ws=1 << 27, wsb=1 << 30), 2, "width"),
+])
+def test_native_bwd_rejects_invalid_arguments(kw, code, msg):
+    lib = _ffi.load()
+    assert _bwd(_NativeAsLib(), **kw) == code
+    assert msg in lib.ccv1d_last_error().decode()
+
+
+def test_native_binding_checks_its_arguments():
+    nat = _native()
+    with pytest.raises(TypeError):
+        nat.fwd(1, 2, 3)
+    with pytest.raises(TypeError):
+        nat.bwd()
+    args = [1 << 20, 0, 8, 2, 1 << 21, 0, None, 0, None, None, 0, 1 << 22, None, 1, 4, 8, 4, 1, 0,
+            None]
+    with pytest.raises(TypeError):
+        nat.fwd(*(args[:3] + ["2"] + args[4:]))
+    with pytest.raises(OverflowError):
+        nat.fwd(*(args[:3] + [1 << 40] + args[4:]))
+
+
+class _NativeAsLib:
+    """Exposes the CPython binding under the C names, for the argument builders above."""
+
+    def ccv1d_fwd(self, *a):
+        return _native().fwd(*a)
+
+    def ccv1d_bwd(self, *a):
+        return _native().bwd(*a)

@@ -342,6 +342,24 @@ def test_final_states_from_either_tile_walk(W, idt):
             assert torch.equal(torch.cat([o1, o2], dim=1), out), (W, B, T)
 
 
+def test_both_bindings_give_identical_results():
+    """The CPython binding and the ctypes binding call the same C functions: identical outputs
+    and gradients, bit for bit."""
+    from causal_conv1d_triton import _ffi
+    inp = make_inputs(21, 2, 300, 512, 4, init=True)
+    native = _ffi._native
+    assert native is not None
+    try:
+        a = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=True)
+        _ffi._native = None
+        b = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=True)
+    finally:
+        _ffi._native = native
+    for k in a:
+        if a[k] is not None:
+            assert torch.equal(a[k], b[k]), k
+
+
 def test_deterministic_weight_grads():
     inp = make_inputs(9, 4, 4096, 1024, 4)
     a = run_gpu(inp, "silu")
