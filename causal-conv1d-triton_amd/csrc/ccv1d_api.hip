@@ -139,9 +139,19 @@ FastShape bwd_shape(int x_dt, int64_t W) {
   return sh;
 }
 
+// Workgroups below which the backward halves its tiles (down to kMinTileRows): a grid with fewer
+// workgroups than CUs is bound by the latency of one wave's walk through its tile, not by
+// bandwidth. Measured at B=4 D=1024 W=4 (fwd+bwd step): T=512 24.6 -> 16.2 us (32 -> 8 rows, 32 ->
+// 128 workgroups), T=2048 28.4 -> 24.2 us (32 -> 16 rows, 128 -> 256 workgroups); the benchmark
+// shape (512 workgroups) keeps 32 rows.
+constexpr int64_t kBwdSmallGrid = 256;
+
 Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
   const FastShape sh = bwd_shape(x_dt, W);
-  return fast_tiling(B, T, D, sh.cpl, sh.nw, 32, kMaxTileRows, 4096, tune().bwd_rows);
+  Tiling t = fast_tiling(B, T, D, sh.cpl, sh.nw, 32, kMaxTileRows, 4096, tune().bwd_rows);
+  while (tune().bwd_rows == 0 && t.nBlk < kBwdSmallGrid && t.L > kMinTileRows)
+    t = fast_tiling(B, T, D, sh.cpl, sh.nw, t.L / 2, t.L / 2, 4096, t.L / 2);
+  return t;
 }
 
 Tiling generic_tiling(int64_t T) {
