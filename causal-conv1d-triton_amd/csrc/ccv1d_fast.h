@@ -126,16 +126,31 @@ struct RowIds {
     const int32_t b = __builtin_amdgcn_readlane(hi, j & 63);
     return j < 64 ? a : b;
   }
-  // True when rows r0 .. r1-1 (r0 < r1 <= r0 + kRowIds) all carry one sequence id and it is not
-  // padding (>= 0). Every sequence mask of such a tile is 1 and no row of it is zeroed, so the tile
-  // can run the kernels' seq_idx-free code, which then gives bit-identical results. The wave votes
-  // need every lane of the wave active.
-  __device__ __forceinline__ bool one_segment(int r1) const {
+  // True when rows r0 .. r1-1 (r0 < r1 <= r0 + kRowIds) all carry the id of row r0. The wave votes
+  // need every lane of the wave active (as in the two tests below).
+  __device__ __forceinline__ bool one_id(int r1) const {
     const int lane = threadIdx.x & 63;
     const int32_t id0 = __builtin_amdgcn_readlane(lo, 0);
-    bool ok = id0 >= 0;
-    ok = __all((r0 + lane < r1 ? lo : id0) == id0) && ok;
+    bool ok = __all((r0 + lane < r1 ? lo : id0) == id0);
     ok = __all((r0 + 64 + lane < r1 ? hi : id0) == id0) && ok;
+    return ok;
+  }
+  // One id and it is not padding (>= 0). Every sequence mask of such a tile is 1 and no row of it
+  // is zeroed, so the tile can run the kernels' seq_idx-free code, which then gives bit-identical
+  // results.
+  __device__ __forceinline__ bool one_segment(int r1) const {
+    return one_id(r1) && __builtin_amdgcn_readlane(lo, 0) >= 0;
+  }
+  // One id and it is padding (< 0): every mask is 1 and every row is zeroed (see bwd_tile's PAD).
+  __device__ __forceinline__ bool one_padding_run(int r1) const {
+    return one_id(r1) && __builtin_amdgcn_readlane(lo, 0) < 0;
+  }
+  // True when every row of [a, b) (r0 <= a, b <= r0 + kRowIds) carries a negative id.
+  __device__ __forceinline__ bool all_padding(int a, int b) const {
+    const int lane = threadIdx.x & 63;
+    const int ra = r0 + lane, rb = r0 + 64 + lane;
+    bool ok = __all(ra < a || ra >= b || lo < 0);
+    ok = __all(rb < a || rb >= b || hi < 0) && ok;
     return ok;
   }
 };
@@ -336,6 +351,7 @@ __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBu
 // start, or both at their end), so the second read finds them in L2 instead of memory.
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int OST>
 __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
+  using IO = VecIO<TX, CPL>;
   constexpr int P = W - 1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -349,6 +365,9 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
   // runs the seq_idx-free code (decided before any lane leaves).
   const RowIds ids = SEQ ? RowIds(p.seq + (int64_t)tc.b * T, t0 - P, T, p.has_init) : RowIds();
   const bool masked = SEQ && !ids.one_segment(t1);
+  // A tile of padding rows only: z = 0 on every row, so every output is silu(0) = +0 (or +0 without
+  // an activation), whatever x holds.
+  const bool pad = masked && ids.all_padding(t0, t1);
   const int grp = tc.gw * 64 + lane;
   if (grp >= p.D / CPL) return;
   const int c0 = grp * CPL;
@@ -360,6 +379,15 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
   const int64_t init_off = (int64_t)tc.b * P * D + c0;
   // final_states (causal_conv1d.py:153-164) come from the registers of the tile ending at T.
   TX* const fin = (p.has_final && t1 == T) ? static_cast<TX*>(p.fin) + init_off : nullptr;
+
+  if (SEQ && pad) {
+    float zero[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) zero[i] = 0.0f;
+    const typename IO::raw zr = IO::pack(zero);
+    for (int t = t0; t < t1; ++t) O.st(t, zr);
+    return;
+  }
 
   if (masked) {
     if (tile & 1) fwd_tile_reverse<TX, W, SILU, SEQ, CPL, R>(p, X, O, ids, c0, t0, t1, fin);
@@ -385,7 +413,9 @@ __global__ __launch_bounds__(NW * 64) void fwd_fast_kernel(const FwdParams p) {
 // one fp32 partial row per workgroup.
 // =============================================================================================
 
-template <typename TX, int W, bool SILU, bool SEQ, int CPL>
+// PAD: every row the lane sees is padding of one sequence id, so g = 0 on every row and every mask
+// is 1: the arithmetic of the masked code on such rows, without dout or the activation.
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, bool PAD = false>
 struct BwdLane {
   using IO = VecIO<TX, CPL>;
   using raw = typename IO::raw;
@@ -428,8 +458,13 @@ struct BwdLane {
                                        float (&dx)[CPL]) {
     float xc[CPL], g[CPL];
     IO::unpack(xr, xc);
-    IO::unpack(yr, g);
-    if (SILU) {
+    if (PAD) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) g[i] = 0.0f;
+    } else {
+      IO::unpack(yr, g);
+    }
+    if (SILU && !PAD) {
       float z[CPL];
       conv_row<W, CPL, SEQ, false>(wv, bv, xw, sw, xc, st, z);
 #pragma unroll
@@ -486,8 +521,10 @@ constexpr int bwd_lds_floats() {
   return halo > red ? halo : red;
 }
 
-// One wave's tile of the backward (the whole kernel but the choice of SEQ, see bwd_fast_kernel).
-template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int YLD, int DXST>
+// One wave's tile of the backward (the whole kernel but the choice of SEQ and PAD, see
+// bwd_fast_kernel). PAD (with SEQ false): a tile inside one run of padding, which reads no dout.
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int YLD, int DXST,
+          bool PAD = false>
 __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const RowIds& ids) {
   using IO = VecIO<TX, CPL>;
   using raw = typename IO::raw;
@@ -519,7 +556,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
   const RowBuf<TX, CPL, YLD> Y(static_cast<const TX*>(p.dy) + (int64_t)tc.b * p.s_yb, p.y_bytes, c0, p.s_yt);
   const RowBuf<TX, CPL, kCachePlain, DXST> DX(static_cast<const TX*>(p.dx) + (int64_t)tc.b * T * D, p.o_bytes, c0, D);
 
-  BwdLane<TX, W, SILU, SEQ, CPL> s;
+  BwdLane<TX, W, SILU, SEQ, CPL, PAD> s;
   s.own_end = own_end;
 #pragma unroll
   for (int k = 0; k < W; ++k)
@@ -552,7 +589,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
     for (int r = 0; r < R; ++r) {
       const int row = min(t + r, t_end - 1);
       bx[r] = X.ld(row);
-      by[r] = Y.ld(row);
+      by[r] = PAD ? raw{} : Y.ld(row);
     }
   };
 
@@ -570,7 +607,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
     for (int q = 0; q < P; ++q) {
       const int row = min(t0 + q, t_end - 1);
       px[q] = X.ld(row);
-      py[q] = Y.ld(row);
+      py[q] = PAD ? raw{} : Y.ld(row);
     }
     load(Ax, Ay, t_main);
     load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
@@ -632,7 +669,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
     }
     for (; t < t_end; ++t) {
       float dx[CPL];
-      s.step(t, X.ld(t), Y.ld(t), SEQ ? ids.at(t) : 0, dx);
+      s.step(t, X.ld(t), PAD ? raw{} : Y.ld(t), SEQ ? ids.at(t) : 0, dx);
       emit_any(t - P, dx);
     }
 
@@ -709,9 +746,11 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
 }
 
 // A wave whose tile (its rows and both halos, t0-P .. own_end+P-1) lies inside one non-padding
-// segment runs the seq_idx-free instantiation of bwd_tile; the others run the masked one. Both have
-// the same LDS barriers, so the waves of one workgroup may take different ones. The host keeps
-// tiles short enough (L + 2 (W - 1) <= kRowIds) for one RowIds to cover a tile and its halos.
+// segment runs the seq_idx-free instantiation of bwd_tile; one whose tile and halos, rows past T
+// included (id -1), lie inside one run of padding runs the PAD instantiation (g = 0 on every row:
+// no dout reads, no activation); the others run the masked one. All three have the same LDS
+// barriers, so the waves of one workgroup may take different ones. The host keeps tiles short
+// enough (L + 2 (W - 1) <= kRowIds) for one RowIds to cover a tile and its halos.
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int YLD, int DXST>
 __global__ __launch_bounds__(NW * 64, (bwd_waves_per_simd<TX, W, CPL>())) void bwd_fast_kernel(
     const BwdParams p) {
@@ -726,8 +765,13 @@ __global__ __launch_bounds__(NW * 64, (bwd_waves_per_simd<TX, W, CPL>())) void b
     // Evaluated on every path (its result is unused past the last tile), so that both id vectors
     // have arrived before either instantiation starts and no wait for them is left to its loop.
     const bool one = ids.one_segment(r1);
+    const bool pad = ids.one_padding_run(t0 + p.tl.L + W - 1);
     if (tile < p.tl.nT && one) {
       bwd_tile<TX, W, SILU, false, CPL, NW, R, XLD, YLD, DXST>(p, lds, ids);
+      return;
+    }
+    if (tile < p.tl.nT && pad) {
+      bwd_tile<TX, W, false, false, CPL, NW, R, XLD, YLD, DXST, true>(p, lds, ids);
       return;
     }
     bwd_tile<TX, W, SILU, SEQ, CPL, NW, R, XLD, YLD, DXST>(p, lds, ids);

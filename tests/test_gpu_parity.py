@@ -280,6 +280,40 @@ def test_seq_idx_long_segments(W):
 
 
 @pytest.mark.parametrize("W", [4, 7])
+def test_seq_idx_padding_runs(W):
+    """Runs of padding long enough to hold whole tiles, which take the padding path (forward: zero
+    stores; backward: g = 0, no dout reads): at the start of a row (with initial states, whose rows
+    then belong to the padding), in the middle with id -3, and at the end with id -2 (rows past T
+    count as id -1, so the tiles whose halo reaches T stay on the masked path); a run of
+    alternating -1/-2 is not one run and stays masked. A non-finite x inside a padding run
+    reaches dweight as NaN (0 * inf), as in the reference."""
+    B, T, D = 3, 3000, 512
+    seq = varlen_seq(60 + W, B, T, lo=100, hi=700, pad_frac=0.0)
+    seq[0, :600] = -1
+    seq[0, -300:] = -1
+    seq[1, 1000:1800] = -3
+    seq[1, -500:] = -2
+    seq[2, 2000:2400] = torch.tensor([-1, -1, -1, -1, -1, -2, -2, -2, -2, -2]).repeat(40)
+    inp = make_inputs(70 + W, B, T, D, W, init=True, seq=seq)
+    gpu = run_gpu(inp, "silu", init_grad=True)
+    compare(gpu, oracle_ref(inp, True, need_dinit=True), True)
+    pad = seq < 0
+    assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0)
+    assert torch.all(gpu["dinit"][0] == 0)  # row 0 starts in padding: no gradient reaches init
+
+    inp["x"][1, 1400, 7] = float("inf")  # inside the -3 run
+    inp["x"][0, 100, 9] = float("nan")   # inside the leading run
+    gpu = run_gpu(inp, "silu", init_grad=True)
+    ref = oracle_ref(inp, True, need_dinit=True)
+    assert torch.equal(gpu["dw"].isnan(), torch.from_numpy(ref["dw"]).isnan())
+    assert gpu["dw"][7].isnan().any() and gpu["dw"][9].isnan().any()
+    assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0)
+    fin = ~gpu["dw"].isnan()
+    torch.testing.assert_close(gpu["dw"][fin], torch.from_numpy(ref["dw"]).float()[fin],
+                               rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("W", [4, 7])
 def test_seq_idx_int64_and_all_equal(W):
     B, T, D = 2, 300, 128
     inp = make_inputs(3, B, T, D, W, init=True)
