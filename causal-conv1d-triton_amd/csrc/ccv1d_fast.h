@@ -3,8 +3,9 @@
 //
 // Work decomposition (both passes): a lane owns CPL consecutive channels, a wave owns 64 such
 // channel vectors over a tile of L consecutive rows, and a workgroup holds NW waves on consecutive
-// tiles of the same channel range. Each wave walks forward in time with the previous width - 1 rows
-// in registers, so a row of x is loaded once per tile plus a (width - 1)-row halo that the
+// tiles of the same channel range. Each wave walks its tile in time (the forward's odd tiles from
+// the end) with a window of width - 1 rows in registers, so a row of x is loaded once per tile plus
+// a (width - 1)-row halo that the
 // neighbouring tile of the same workgroup (same CU) or of the same XCD (xcd_remap) has just read.
 // Rows are processed in batches of R: the loads of batch k + 1 are issued before batch k is
 // computed, so every wave keeps up to 2R rows of reads in flight while its ALUs work.
