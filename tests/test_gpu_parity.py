@@ -394,6 +394,46 @@ def test_both_bindings_give_identical_results():
             assert torch.equal(a[k], b[k]), k
 
 
+def _random_seq(g, B, T):
+    """Segments of random lengths with ids that mostly increase, sometimes repeat an earlier id or
+    go negative (padding runs with ids -1 or -2), so that tiles of every kind occur: inside one
+    segment, across boundaries, inside one padding run, and across mixed padding."""
+    s = torch.empty(B, T, dtype=torch.int32)
+    for b in range(B):
+        t, sid = 0, 0
+        while t < T:
+            n = int(torch.randint(1, max(2, T // 3), (1,), generator=g))
+            u = float(torch.rand(1, generator=g))
+            s[b, t:t + n] = -1 if u < 0.2 else (-2 if u < 0.25 else (max(sid - 1, 0) if u < 0.3
+                                                                       else sid))
+            t, sid = t + n, sid + 1
+    return s
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_cases(case):
+    """Random shapes, widths, dtypes and options (bias, activation, initial states, seq_idx with
+    padding runs, final states with their gradient) against the oracle."""
+    g = _gen(1000 + case)
+    pick = lambda opts: opts[int(torch.randint(0, len(opts), (1,), generator=g))]  # noqa: E731
+    B = pick([1, 2, 3, 4])
+    T = pick([1, 2, 5, 9, 17, 64, 100, 333, 700])
+    D = pick([8, 64, 100, 256, 264, 1000, 1024])
+    W = pick([2, 3, 4, 5, 6, 7, 8, 9])
+    xdt = pick([torch.bfloat16, torch.bfloat16, torch.float16, torch.float32])
+    bias, silu, init = pick([True, False]), pick([True, False]), pick([True, False])
+    seq = _random_seq(g, B, T) if pick([True, False]) else None
+    final = seq is None and pick([True, False])
+    inp = make_inputs(2000 + case, B, T, D, W, xdt=xdt, bias=bias, init=init, seq=seq)
+    act = "silu" if silu else None
+    gpu = run_gpu(inp, act, return_final=final, dfinal=final, init_grad=init)
+    ref = oracle_ref(inp, silu, final=final, dfinal=final, need_dinit=init)
+    compare(gpu, ref, silu)
+    if seq is not None:
+        pad = seq < 0
+        assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0), case
+
+
 def test_deterministic_weight_grads():
     inp = make_inputs(9, 4, 4096, 1024, 4)
     a = run_gpu(inp, "silu")
