@@ -7,8 +7,10 @@ out = causal_conv1d_fn(x, w, b, activation="silu") followed by the gradients of 
 (torch.autograd.grad, so nothing is accumulated). Input sets rotate (4 sets of x and dy, 512 MiB, twice
 the 256 MiB Infinity Cache) so every step reads its inputs from HBM. Steps are captured once per input
 set into one HIP graph (a replay runs one step per input set back to back) and replayed, which removes
-Python launch overhead from the device timeline. The time of each pass inside the step (the roofline
-entry) comes from events between the passes of eager steps that make the same launches.
+Python launch overhead from the device timeline. The time of each pass inside the step comes from
+events between the passes of eager steps that make the same launches, and the time of each pass's
+main kernel (the roofline entry: the backward kernel) from events HIP sets to those kernels' own
+dispatch start and end in other eager steps.
 Every timed region follows at least --warmup steps and at least 50 ms of untimed replays, so it
 measures the device's steady state rather than its clock ramp after idle.
 
@@ -40,6 +42,12 @@ def alg_bytes(B, T, D, W, ex=2, ew=4, eb=4):
     fwd = n * (ex + ex) + D * W * ew + D * eb
     bwd = n * (ex + ex + ex) + 2 * D * W * ew + 2 * D * eb
     return fwd, bwd
+
+
+def bwd_kernel_alg_bytes(B, T, D, W, ex=2, ew=4, eb=4):
+    """Algorithmic bytes of the backward pass's main kernel: x and dout read, dx written, weights
+    and bias read. dweight and dbias are written by the reduction that follows it."""
+    return B * T * D * (ex + ex + ex) + D * W * ew + D * eb
 
 
 def _capture(fn, warm_stream):
@@ -86,25 +94,34 @@ def _time_graphs(seq):
 
 
 def passes_in_step(sets, w, b, steps):
-    """Mean device time of the forward and of the backward pass inside fwd+bwd steps, and of the
-    step. The steps run eagerly through the launches causal_conv1d_fn and its autograd backward make
-    (_fwd, then _bwd: the same kernels on the same stream), with HIP events on the launch stream
-    before the forward, between the passes and after the backward. All measured steps are queued
-    behind a bounded spin kernel (torch.cuda._sleep) that keeps the device busy while the host
-    enqueues them, so the device then runs them back to back without waiting for the host and each
-    event interval is device time only. Returns {"fwd": ms, "bwd": ms, "step": ms}."""
+    """Mean device time of the forward and of the backward pass inside fwd+bwd steps, of the step,
+    and of each pass's main kernel. The steps run eagerly through the launches causal_conv1d_fn and
+    its autograd backward make (_fwd, then _bwd: the same kernels on the same stream). On some steps
+    HIP events are recorded on the launch stream before the forward, between the passes and after
+    the backward (pass times); on other steps no event packet is queued, and the library is asked
+    (ccv1d_time_main_kernel) to launch the forward and the backward kernel with events that HIP sets
+    from those dispatches' own start and end timestamps (kernel times, the same quantity a
+    rocprofv3 kernel trace records). All measured steps are queued behind a bounded spin kernel
+    (torch.cuda._sleep) that keeps the device busy while the host enqueues them, so the device then
+    runs them back to back without waiting for the host and each interval is device time only.
+    Returns {"fwd": ms, "bwd": ms, "step": ms, "fwd_kernel": ms, "bwd_kernel": ms}."""
+    from causal_conv1d_triton import _ffi
     from causal_conv1d_triton.causal_conv1d import _bwd, _fwd
 
     n = len(sets)
     wd, bd = w.detach(), b.detach()
 
-    def step(i, ev=None):
+    def step(i, ev=None, kev=None):
         x, dy = sets[i % n]
         if ev:
             ev[0].record()
+        if kev:
+            _ffi.time_main_kernel(kev[0], kev[1])
         _fwd(x.detach(), wd, bd, None, None, None, True)
         if ev:
             ev[1].record()
+        if kev:
+            _ffi.time_main_kernel(kev[2], kev[3])
         r = _bwd(x.detach(), wd, bd, None, None, dy, None, False, True)
         if ev:
             ev[2].record()
@@ -132,6 +149,11 @@ def passes_in_step(sets, w, b, steps):
     steps = max(steps, 2 * every)
     evs = {i: [torch.cuda.Event(enable_timing=True) for _ in range(3)]
            for i in range(steps) if i % every == every - 1}
+    kevs = {i: [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            for i in range(steps) if i % every == every // 2 - 1}
+    for kev in kevs.values():
+        for e in kev:
+            e.record()  # torch creates the HIP event at its first record
     first, last = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     # queue some warm steps, then the spin, then the measured steps, so the device is busy and warm
     for i in range(16):
@@ -141,14 +163,17 @@ def passes_in_step(sets, w, b, steps):
     for i in range(steps + skip):
         if i == skip:
             first.record()
-        step(i, evs.get(i - skip))
+        step(i, evs.get(i - skip), kevs.get(i - skip))
     last.record()
     torch.cuda.synchronize()
     use = list(evs.values())
     fwd = sum(e[0].elapsed_time(e[1]) for e in use) / len(use)
     bwd = sum(e[1].elapsed_time(e[2]) for e in use) / len(use)
+    kuse = list(kevs.values())
+    fwd_k = sum(e[0].elapsed_time(e[1]) for e in kuse) / len(kuse)
+    bwd_k = sum(e[2].elapsed_time(e[3]) for e in kuse) / len(kuse)
     step_ms = first.elapsed_time(last) / steps
-    return {"fwd": fwd, "bwd": bwd, "step": step_ms}
+    return {"fwd": fwd, "bwd": bwd, "step": step_ms, "fwd_kernel": fwd_k, "bwd_kernel": bwd_k}
 
 
 def calibrate_copy(dev, mib=256, reps=3):
@@ -464,9 +489,16 @@ def main():
         isolated = {"fwd": round(iso_fwd * 1e3, 2), "bwd": round(iso_bwd * 1e3, 2)}
 
     fwd_b, bwd_b = alg_bytes(B, T, D, W)
+    bk_b = bwd_kernel_alg_bytes(B, T, D, W)
     gbs = (fwd_b + bwd_b) / (ms_step * 1e-3) / 1e9
     bwd_gbs = bwd_b / (ms_bwd * 1e-3) / 1e9
+    ms_bk = ms_pass["bwd_kernel"]
+    bk_gbs = bk_b / (ms_bk * 1e-3) / 1e9
     tr = traffic_from_profiles()
+    bk_traffic = None
+    if tr is not None:
+        k = tr["per_kernel_bytes"]["bwd_fast_kernel"]
+        bk_traffic = k["read"] + k["write"]
     line = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -493,21 +525,29 @@ def main():
         "passes_in_step_us": {"fwd": round(ms_fwd * 1e3, 2), "bwd": round(ms_bwd * 1e3, 2)},
         "passes_in_step_gbs": {"fwd": round(fwd_b / (ms_fwd * 1e-3) / 1e9, 1),
                                "bwd": round(bwd_gbs, 1)},
+        "kernels_in_step_us": {"fwd_fast_kernel": round(ms_pass["fwd_kernel"] * 1e3, 2),
+                               "bwd_fast_kernel": round(ms_bk * 1e3, 2)},
         "eager_step_us": round(ms_pass["step"] * 1e3, 2),
         "passes_isolated_us": isolated,
         "roofline": {
-            "kernel": "backward pass (bwd_fast_kernel + reduce_partials_kernel)",
-            "measured": "HIP events on the launch stream around the backward pass of every 4th "
-                        f"of {args.steps} eager fwd+bwd steps queued back to back (mean)",
-            "launch_us": round(ms_bwd * 1e3, 2),
+            "kernel": "bwd_fast_kernel (the backward pass's main kernel; reduce_partials_kernel "
+                      "then sums its partials into dweight/dbias)",
+            "measured": "events set by HIP from the kernel dispatch's own start and end timestamps "
+                        "(ccv1d_time_main_kernel, hipExtLaunchKernel) on every 4th of "
+                        f"{args.steps} eager fwd+bwd steps queued back to back (mean)",
+            "launch_us": round(ms_bk * 1e3, 2),
             "bound": "hbm",
-            "achieved": round(bwd_gbs, 1),
+            "achieved": round(bk_gbs, 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(bwd_gbs / PEAK_GBS, 4),
-            "traffic": None if tr is None else tr["bwd_pass_bytes"],
+            "frac": round(bk_gbs / PEAK_GBS, 4),
+            "traffic": bk_traffic,
             "traffic_source": None if tr is None else tr["source"],
-            "alg_bytes": bwd_b,
+            "alg_bytes": bk_b,
+            "pass": {"launches": "bwd_fast_kernel + reduce_partials_kernel",
+                     "us": round(ms_bwd * 1e3, 2), "alg_bytes": bwd_b,
+                     "achieved": round(bwd_gbs, 1), "frac": round(bwd_gbs / PEAK_GBS, 4),
+                     "traffic": None if tr is None else tr["bwd_pass_bytes"]},
         },
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
     }

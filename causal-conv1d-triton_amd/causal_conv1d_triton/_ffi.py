@@ -65,6 +65,8 @@ def load() -> ctypes.CDLL:
         _c_i64, _c_i64, _c_i64, _c_i64,  # batch, seqlen, dim, width
         _c_int, _c_int, _c_ptr,  # silu, device, stream
     ]
+    lib.ccv1d_time_main_kernel.restype = _c_int
+    lib.ccv1d_time_main_kernel.argtypes = [_c_ptr, _c_ptr]
     lib.ccv1d_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.ccv1d_bwd_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]
     lib.ccv1d_bwd.restype = _c_int
@@ -134,6 +136,17 @@ def fwd(x, weight, bias, seq_idx, initial_states, out, final_states, silu: bool)
         rc = (_lib if _lib is not None else load()).ccv1d_fwd(*args)
     if rc:
         _check(rc, load())
+
+
+def time_main_kernel(start, stop) -> None:
+    """Asks the calling thread's next fwd or bwd call to time its main kernel with two
+    torch.cuda.Event(enable_timing=True): afterwards start.elapsed_time(stop) is that kernel's own
+    execution time (ccv1d_time_main_kernel in include/ccv1d.h). torch creates an event's HIP handle
+    at its first record, so each event must have been recorded once before."""
+    if not (start.cuda_event and stop.cuda_event):
+        raise ValueError("record each event once before using it for kernel timing")
+    lib = load()
+    _check(lib.ccv1d_time_main_kernel(start.cuda_event, stop.cuda_event), lib)
 
 
 def bwd_workspace_bytes(B: int, T: int, D: int, W: int, x_dtype: torch.dtype) -> int:

@@ -216,6 +216,23 @@ uint32_t slab_bytes(int x_dt, int64_t T, int64_t D, int64_t s_t) {
 
 bool fast_dtype(int x_dt, int64_t W) { return W <= kMaxFastW && x_dt != CCV1D_F64; }
 
+// Takes the calling thread's timing request (ccv1d_time_main_kernel), so that it applies to this
+// entry-point call only, whatever the call does.
+bool take_timing_request() {
+  KernelEvents& ev = kernel_events();
+  const bool on = ev.pending;
+  ev.pending = false;
+  ev.armed = false;
+  return on;
+}
+
+// Hands a taken timing request to the main kernel's launch for the lifetime of this object (one
+// launch takes it; it is cleared on scope exit in case the launch was not reached).
+struct TimedLaunch {
+  explicit TimedLaunch(bool on) { kernel_events().armed = on; }
+  ~TimedLaunch() { kernel_events().armed = false; }
+};
+
 }  // namespace
 
 extern "C" {
@@ -224,12 +241,25 @@ int ccv1d_abi_version(void) { return CCV1D_ABI_VERSION; }
 
 const char* ccv1d_last_error(void) { return g_last_error.c_str(); }
 
+int ccv1d_time_main_kernel(void* start_event, void* stop_event) {
+  g_last_error.clear();
+  if ((start_event == nullptr) != (stop_event == nullptr))
+    return fail(CCV1D_ERR_INVALID, "give both timing events or neither");
+  KernelEvents& ev = kernel_events();
+  ev.start = static_cast<hipEvent_t>(start_event);
+  ev.stop = static_cast<hipEvent_t>(stop_event);
+  ev.pending = start_event != nullptr;
+  ev.armed = false;
+  return CCV1D_OK;
+}
+
 int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
               const void* weight, int weight_dtype, const void* bias, int bias_dtype,
               const int32_t* seq_idx, const void* initial_states, int init_dtype, void* out,
               void* final_states, int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
               int silu, int device, void* stream) {
   g_last_error.clear();
+  const bool timed = take_timing_request();
   const int64_t B = batch, T = seqlen, D = dim, W = width, P = W - 1;
   int rc = check_common(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
                         initial_states, init_dtype, B, T, D, W);
@@ -295,18 +325,21 @@ int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
 
   p.tl = tl;
   hipError_t e;
-  if (fast) {
-    switch (x_dtype) {
-      case CCV1D_BF16: e = launch_fwd_fast_t<__bf16>(p, s); break;
-      case CCV1D_F16: e = launch_fwd_fast_t<_Float16>(p, s); break;
-      default: e = launch_fwd_fast_t<float>(p, s); break;
-    }
-  } else {
-    switch (x_dtype) {
-      case CCV1D_BF16: e = launch_fwd_generic_t<__bf16>(p, s); break;
-      case CCV1D_F16: e = launch_fwd_generic_t<_Float16>(p, s); break;
-      case CCV1D_F32: e = launch_fwd_generic_t<float>(p, s); break;
-      default: e = launch_fwd_generic_t<double>(p, s); break;
+  {
+    const TimedLaunch timing(timed);
+    if (fast) {
+      switch (x_dtype) {
+        case CCV1D_BF16: e = launch_fwd_fast_t<__bf16>(p, s); break;
+        case CCV1D_F16: e = launch_fwd_fast_t<_Float16>(p, s); break;
+        default: e = launch_fwd_fast_t<float>(p, s); break;
+      }
+    } else {
+      switch (x_dtype) {
+        case CCV1D_BF16: e = launch_fwd_generic_t<__bf16>(p, s); break;
+        case CCV1D_F16: e = launch_fwd_generic_t<_Float16>(p, s); break;
+        case CCV1D_F32: e = launch_fwd_generic_t<float>(p, s); break;
+        default: e = launch_fwd_generic_t<double>(p, s); break;
+      }
     }
   }
   if (e != hipSuccess) return hip_fail(e, "forward launch");
@@ -333,6 +366,7 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
               void* dbias, void* workspace, size_t workspace_bytes, int64_t batch, int64_t seqlen,
               int64_t dim, int64_t width, int silu, int device, void* stream) {
   g_last_error.clear();
+  const bool timed = take_timing_request();
   const int64_t B = batch, T = seqlen, D = dim, W = width, P = W - 1;
   int rc = check_common(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
                         initial_states, init_dtype, B, T, D, W);
@@ -425,18 +459,21 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
 
   p.tl = tl;
   hipError_t e;
-  if (fast) {
-    switch (x_dtype) {
-      case CCV1D_BF16: e = launch_bwd_fast_t<__bf16>(p, s); break;
-      case CCV1D_F16: e = launch_bwd_fast_t<_Float16>(p, s); break;
-      default: e = launch_bwd_fast_t<float>(p, s); break;
-    }
-  } else {
-    switch (x_dtype) {
-      case CCV1D_BF16: e = launch_bwd_generic_t<__bf16>(p, s); break;
-      case CCV1D_F16: e = launch_bwd_generic_t<_Float16>(p, s); break;
-      case CCV1D_F32: e = launch_bwd_generic_t<float>(p, s); break;
-      default: e = launch_bwd_generic_t<double>(p, s); break;
+  {
+    const TimedLaunch timing(timed);
+    if (fast) {
+      switch (x_dtype) {
+        case CCV1D_BF16: e = launch_bwd_fast_t<__bf16>(p, s); break;
+        case CCV1D_F16: e = launch_bwd_fast_t<_Float16>(p, s); break;
+        default: e = launch_bwd_fast_t<float>(p, s); break;
+      }
+    } else {
+      switch (x_dtype) {
+        case CCV1D_BF16: e = launch_bwd_generic_t<__bf16>(p, s); break;
+        case CCV1D_F16: e = launch_bwd_generic_t<_Float16>(p, s); break;
+        case CCV1D_F32: e = launch_bwd_generic_t<float>(p, s); break;
+        default: e = launch_bwd_generic_t<double>(p, s); break;
+      }
     }
   }
   if (e != hipSuccess) return hip_fail(e, "backward launch");

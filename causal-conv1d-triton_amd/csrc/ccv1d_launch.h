@@ -3,6 +3,8 @@
 // translation unit of their own (ccv1d_fast_<dtype>.hip) so they compile in parallel.
 #pragma once
 
+#include <hip/hip_ext.h>
+
 #include "ccv1d_device.h"
 
 namespace ccv1d {
@@ -43,9 +45,27 @@ constexpr int kMaxGenericW = 128;  // LDS ring of the generic backward: 2 * W * 
 constexpr int kReduceNW = 16;    // waves per reduction workgroup
 constexpr int kGenericL = 64;    // rows per tile of the generic kernels
 
+// Timing events of the calling thread (ccv1d_time_main_kernel). `pending` holds a request for the
+// thread's next entry-point call, which takes it; the call sets `armed` right before its main kernel
+// and clears it after, and launch() gives an armed pair to that one launch.
+struct KernelEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+  bool pending = false, armed = false;
+};
+inline KernelEvents& kernel_events() {
+  static thread_local KernelEvents e;
+  return e;
+}
+
 inline hipError_t launch(const void* kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t s,
                          const void* params) {
   void* args[] = {const_cast<void*>(params)};
+  KernelEvents& ev = kernel_events();
+  if (ev.armed) {
+    // HIP sets both events from the dispatch's own start and end timestamps.
+    ev.armed = false;
+    return hipExtLaunchKernel(kernel, grid, block, args, shmem, s, ev.start, ev.stop, 0);
+  }
   return hipLaunchKernel(kernel, grid, block, args, shmem, s);
 }
 

@@ -23,8 +23,8 @@
  *  - Offsets inside one batch element are 32-bit: (seqlen + width) * max(x_stride_t, dim) and the same
  *    for dout must be below 2^31.
  *  - Return value: CCV1D_OK (0) or an error code; ccv1d_last_error() then describes the failure.
- *  - Reentrant and thread-safe; the only global state is the error string (thread-local) and a tuning
- *    table read once from the environment.
+ *  - Reentrant and thread-safe; the only global state is the error string and the timing request of
+ *    ccv1d_time_main_kernel (both thread-local) and a tuning table read once from the environment.
  */
 #ifndef CCV1D_H
 #define CCV1D_H
@@ -56,6 +56,18 @@ int ccv1d_abi_version(void);
 
 /* Description of the last error raised on the calling thread ("" if none). */
 const char* ccv1d_last_error(void);
+
+/* Measurement aid; it has no counterpart in the reference, whose passes are timed from Python
+ * around whole launches. Asks the calling thread's next ccv1d_fwd or ccv1d_bwd call to launch its
+ * main kernel (the convolution kernel of the pass; not the dweight/dbias reduction or a fill)
+ * through hipExtLaunchKernel with these two events, which HIP sets from that dispatch's own start
+ * and end timestamps: once the kernel has completed, hipEventElapsedTime(start_event, stop_event)
+ * is its execution time, without the marker packets of hipEventRecord around it. The events are
+ * hipEvent_t handles with timing enabled, created by the caller. The request applies to the next
+ * call only, whatever that call does; a call that launches no main kernel (empty input, an error)
+ * leaves the events as they were. Not meant for stream capture. Two NULLs cancel a pending request;
+ * exactly one NULL is CCV1D_ERR_INVALID. */
+int ccv1d_time_main_kernel(void* start_event, void* stop_event);
 
 /* Forward pass. Replaces the host launcher `_fwd` of the reference
  * (causal_conv1d_triton/causal_conv1d.py:433-472) together with the `_fwd_kernel` it launches

@@ -27,7 +27,7 @@ def _declared():
 
 def test_header_declares_the_entry_points():
     assert _declared() == ["ccv1d_abi_version", "ccv1d_bwd", "ccv1d_bwd_workspace_bytes",
-                           "ccv1d_fwd", "ccv1d_last_error"]
+                           "ccv1d_fwd", "ccv1d_last_error", "ccv1d_time_main_kernel"]
 
 
 def test_library_exports_every_declared_symbol():
@@ -110,6 +110,27 @@ def test_bwd_rejects_invalid_arguments(kw, code, msg):
     lib = _ffi.load()
     assert _bwd(lib, **kw) == code
     assert msg in lib.ccv1d_last_error().decode()
+
+
+def test_timing_request_needs_both_events_or_neither():
+    lib = _ffi.load()
+    assert lib.ccv1d_time_main_kernel(1 << 20, None) == 1
+    assert "both timing events" in lib.ccv1d_last_error().decode()
+    assert lib.ccv1d_time_main_kernel(None, 1 << 20) == 1
+    assert lib.ccv1d_time_main_kernel(None, None) == 0
+    assert lib.ccv1d_last_error().decode() == ""
+    # A request (here with stand-in handles that must never reach HIP) is taken by the next call,
+    # which fails validation and so launches nothing; the cancel after it leaves nothing pending.
+    assert lib.ccv1d_time_main_kernel(1 << 20, 1 << 21) == 0
+    assert _fwd(lib, W=1) == 1
+    assert lib.ccv1d_time_main_kernel(None, None) == 0
+
+
+def test_timing_helper_needs_created_events():
+    class Unrecorded:
+        cuda_event = 0
+    with pytest.raises(ValueError, match="record each event"):
+        _ffi.time_main_kernel(Unrecorded(), Unrecorded())
 
 
 # The package's CPython binding of the two launch entry points (csrc/ccv1d_pyext.c): same C

@@ -394,6 +394,52 @@ def test_both_bindings_give_identical_results():
             assert torch.equal(a[k], b[k]), k
 
 
+@pytest.mark.parametrize("W,xdt", [(4, torch.bfloat16), (12, torch.bfloat16), (4, torch.float64)])
+def test_kernel_timing_events(W, xdt):
+    """ccv1d_time_main_kernel (fast and generic kernels): the timed launch gives bit-identical
+    results, sets both events to a positive kernel time inside the interval of events recorded
+    around the call, and covers one call only (an untimed call after it leaves the events as they
+    were)."""
+    from causal_conv1d_triton import _ffi
+
+    B, T, D = 2, 700, 256
+    inp = make_inputs(22, B, T, D, W, xdt=xdt)
+    x, w, b, dy = (inp[k].to(DEV) for k in ("x", "w", "b", "dy"))
+    ws = torch.empty(_ffi.bwd_workspace_bytes(B, T, D, W, xdt), dtype=torch.uint8, device=DEV)
+
+    def fwd():
+        out = torch.empty_like(x)
+        _ffi.fwd(x, w, b, None, None, out, None, True)
+        return out
+
+    def bwd():
+        dx, dw, db = torch.empty_like(x), torch.empty_like(w), torch.empty_like(b)
+        _ffi.bwd(x, w, b, None, None, dy, None, dx, None, dw, db, ws, True)
+        return dx, dw, db
+
+    want_out, want_grads = fwd(), bwd()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+    for e in ev:
+        e.record()  # creates the HIP events
+    ev[4].record()
+    _ffi.time_main_kernel(ev[0], ev[1])
+    out = fwd()
+    ev[5].record()
+    _ffi.time_main_kernel(ev[2], ev[3])
+    grads = bwd()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want_out)
+    for got, want in zip(grads, want_grads):
+        assert torch.equal(got, want)
+    t_fwd, t_bwd = ev[0].elapsed_time(ev[1]), ev[2].elapsed_time(ev[3])
+    assert 0 < t_fwd <= ev[4].elapsed_time(ev[5])
+    assert 0 < t_bwd
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    assert ev[0].elapsed_time(ev[1]) == t_fwd and ev[2].elapsed_time(ev[3]) == t_bwd
+
+
 def _random_seq(g, B, T):
     """Segments of random lengths with ids that mostly increase, sometimes repeat an earlier id or
     go negative (padding runs with ids -1 or -2), so that tiles of every kind occur: inside one
