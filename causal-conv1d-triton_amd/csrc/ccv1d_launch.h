@@ -101,21 +101,27 @@ constexpr int bwd_cpl() {
   return W >= kBwdWideW ? BwdCfg<TX>::CPL_WIDE : BwdCfg<TX>::CPL;
 }
 
-// The backward's batch depth: C::R rows where the register budget of 4 waves per SIMD holds it
-// (rows of at most 8 bytes, width <= 4), else 2 rows, which keeps the wider and fp32 instances
-// from spilling.
-template <typename TX, int W>
+// The backward's batch depth: C::R rows where the register budget holds it, else 2 rows, which
+// keeps the other instances from spilling. C::R fits at widths <= 4 with rows of at most 8 bytes
+// (4 waves per SIMD), and from kBwdWideW up with 16- and 8-bit types (2 channels per lane, 4-byte
+// rows: 88-104 VGPRs) except with seq_idx, whose kernel also holds the sequence ids. Measured
+// (fwd+bwd step, bf16, R = 4 against 2): B=4 T=8192 D=1024 W=6 -1.2 %, W=7 -2.8 %, W=8 -2.5 %;
+// B=8 T=4096 D=5376 W=8 -0.4 %; with seq_idx (B=4 T=16384 D=4096 W=7) +1 %, hence 2 there. Width 5
+// with 4 rows spills.
+template <typename TX, int W, bool SEQ>
 constexpr int bwd_rows() {
   using C = BwdCfg<TX>;
-  return (W <= 4 && C::CPL * (int)sizeof(TX) <= 8) ? C::R : 2;
+  if (W <= 4 && C::CPL * (int)sizeof(TX) <= 8) return C::R;
+  if (W >= kBwdWideW && !SEQ && C::CPL_WIDE * (int)sizeof(TX) <= 4) return C::R;
+  return 2;
 }
 
 template <typename TX, int W, bool SILU, bool SEQ>
 static hipError_t bwd_one(const BwdParams& p, hipStream_t s) {
   using C = BwdCfg<TX>;
   return launch(reinterpret_cast<const void*>(
-                    &bwd_fast_kernel<TX, W, SILU, SEQ, bwd_cpl<TX, W>(), C::NW, bwd_rows<TX, W>(),
-                                     C::XLD, C::YLD, C::DXST>),
+                    &bwd_fast_kernel<TX, W, SILU, SEQ, bwd_cpl<TX, W>(), C::NW,
+                                     bwd_rows<TX, W, SEQ>(), C::XLD, C::YLD, C::DXST>),
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
 }
 
