@@ -276,11 +276,13 @@ def _alg_bytes_general(B, T, D, W, bias, init=False, seq=False, final=False, ex=
     return fwd, bwd
 
 
-def run_configs(dev):
+def run_configs(dev, widths=False):
     """One JSON line per BASELINE configuration 2-5 (the reference's README sweep, the Mamba-2 xBC
     shape, chunked streaming and decode with state handoff, packed varlen seq_idx): device time per
     call from replayed graphs after the usual warm-up, plus, for the latency-bound streaming and
-    decode calls, the host-inclusive eager time per call."""
+    decode calls, the host-inclusive eager time per call. With `widths`, instead: the benchmark
+    shape (bf16, bias + silu) at every width the vectorised kernels cover, forward alone and
+    forward + backward."""
     from causal_conv1d_triton import causal_conv1d_fn
     from causal_conv1d_triton.causal_conv1d import _fwd
 
@@ -325,6 +327,21 @@ def run_configs(dev):
         g = _capture(fn, side)
         res.clear()
         return g
+
+    if widths:
+        B, T, D = 4, 8192, 1024
+        sets = [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
+                 .requires_grad_(True),
+                 torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
+                for _ in range(4)]
+        b = torch.randn(D, generator=gen, device=dev).requires_grad_(True)
+        for W in range(2, 9):
+            w = (torch.randn(D, W, generator=gen, device=dev) / math.sqrt(W)).requires_grad_(True)
+            fb, bb = _alg_bytes_general(B, T, D, W, True)
+            shape = f"B={B} T={T} D={D} W={W} bias_silu"
+            emit("widths", shape, timed(fwds(sets, w, b, "silu"), len(sets)), fb, bb, "fwd")
+            emit("widths", shape, timed(steps(sets, w, b, "silu"), len(sets)), fb, bb, "fwd+bwd")
+        return
 
     # Configuration 2: README shape sweep, B=4 D=1024 W=4, weight only or bias + silu.
     for T in (512, 2048, 8192, 32768):
@@ -423,6 +440,8 @@ def main():
                     help="also time each pass alone (graphs of one pass per input set)")
     ap.add_argument("--configs", action="store_true",
                     help="instead of the headline line, one JSON line per BASELINE configuration 2-5")
+    ap.add_argument("--widths", action="store_true",
+                    help="instead of the headline line, the benchmark shape at widths 2-8")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -436,8 +455,8 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    if args.configs:
-        run_configs(dev)
+    if args.configs or args.widths:
+        run_configs(dev, widths=args.widths)
         return
     B, T, D, W = 4, 8192, 1024, 4
     gen = torch.Generator(device=dev).manual_seed(0)

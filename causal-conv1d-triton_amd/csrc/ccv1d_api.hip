@@ -89,6 +89,9 @@ const Tune& tune() {
 // better (248 vs 251 us).
 constexpr int64_t kMinTimeWorkgroups = 16;
 
+// Waves the vectorised kernels' tilings aim for (16 per CU).
+constexpr int64_t kTargetWaves = 4096;
+
 // Tiling of the vectorised kernels: the longest tile (fewest halo re-reads) that still gives the
 // grid `target_waves` waves and every column kMinTimeWorkgroups workgroups along time, a function
 // of the shape alone so that results, including the dweight summation order, do not depend on the
@@ -110,6 +113,7 @@ Tiling fast_tiling(int64_t B, int64_t T, int64_t D, int vec, int nw, int lmin, i
   t.nT = (int32_t)cdiv(T, L);
   t.nTB = (int32_t)cdiv(t.nT, nw);
   t.nBlk = (int32_t)(B * t.nGW * t.nTB);
+  t.vec = vec;
   return t;
 }
 
@@ -120,23 +124,10 @@ constexpr int64_t kFwdSmallGrid = 256;
 
 Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
   const FastShape sh = shape_of<FwdCfg>(x_dt);
-  Tiling t = fast_tiling(B, T, D, sh.cpl, sh.nw, 16, kMaxTileRows, 4096, tune().fwd_rows);
+  Tiling t = fast_tiling(B, T, D, sh.cpl, sh.nw, 16, kMaxTileRows, kTargetWaves, tune().fwd_rows);
   if (tune().fwd_rows == 0 && t.L == 16 && t.nBlk < kFwdSmallGrid)
-    t = fast_tiling(B, T, D, sh.cpl, sh.nw, kMinTileRows, kMinTileRows, 4096, kMinTileRows);
+    t = fast_tiling(B, T, D, sh.cpl, sh.nw, kMinTileRows, kMinTileRows, kTargetWaves, kMinTileRows);
   return t;
-}
-
-// Channels per lane and waves per workgroup of the vectorised backward at width W.
-FastShape bwd_shape(int x_dt, int64_t W) {
-  FastShape sh = shape_of<BwdCfg>(x_dt);
-  if (W >= kBwdWideW) {
-    switch (x_dt) {
-      case CCV1D_BF16: sh.cpl = BwdCfg<__bf16>::CPL_WIDE; break;
-      case CCV1D_F16: sh.cpl = BwdCfg<_Float16>::CPL_WIDE; break;
-      default: sh.cpl = BwdCfg<float>::CPL_WIDE; break;
-    }
-  }
-  return sh;
 }
 
 // Workgroups below which the backward halves its tiles (down to kMinTileRows): a grid with fewer
@@ -146,12 +137,50 @@ FastShape bwd_shape(int x_dt, int64_t W) {
 // shape (512 workgroups) keeps 32 rows.
 constexpr int64_t kBwdSmallGrid = 256;
 
-Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
-  const FastShape sh = bwd_shape(x_dt, W);
-  Tiling t = fast_tiling(B, T, D, sh.cpl, sh.nw, 32, kMaxTileRows, 4096, tune().bwd_rows);
+Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int cpl, int nw) {
+  Tiling t = fast_tiling(B, T, D, cpl, nw, 32, kMaxTileRows, kTargetWaves, tune().bwd_rows);
   while (tune().bwd_rows == 0 && t.nBlk < kBwdSmallGrid && t.L > kMinTileRows)
-    t = fast_tiling(B, T, D, sh.cpl, sh.nw, t.L / 2, t.L / 2, 4096, t.L / 2);
+    t = fast_tiling(B, T, D, cpl, nw, t.L / 2, t.L / 2, kTargetWaves, t.L / 2);
   return t;
+}
+
+// The vectorised backward of 16-bit x at widths under kBwdWideW takes 2 channels per lane instead
+// of 4 when the 4-channel grid is small: fewer than kTargetWaves waves, or tiles shortened below
+// kBwdNarrowMinRows rows to reach them. 2 channels per lane doubles the waves while keeping the
+// tiles longer. Measured (fwd+bwd step, bf16, 2 against 4 channels): B=4 D=1024 W=4 T=512 16.2 ->
+// 13.8 us, T=2048 24.1 -> 22.5, T=4096 39.9 -> 37.2; B=2 T=8192 D=1024 38.8 -> 36.8; W=2 T=512
+// 15.2 -> 13.8; W=3 T=2048 23.3 -> 22.1; W=5 T=2048 25.1 -> 22.9. Grids that reach the target with
+// 32- or 64-row tiles keep 4 channels (B=4 D=1024 T=32768: 250 against 256-258 us; B=1 T=8192
+// D=4096: 61.0 against 61.5; the benchmark shape: a tie at 32 rows, 62.3 us when 2 channels pick
+// 64-row tiles).
+constexpr int kBwdNarrowMinRows = 32;
+
+int cpl_wide(int x_dt) {
+  switch (x_dt) {
+    case CCV1D_BF16: return BwdCfg<__bf16>::CPL_WIDE;
+    case CCV1D_F16: return BwdCfg<_Float16>::CPL_WIDE;
+    default: return BwdCfg<float>::CPL_WIDE;
+  }
+}
+
+// Channels per lane and waves per workgroup of the vectorised backward for a shape: CPL_WIDE from
+// kBwdWideW up (register budget), and for 16-bit x when the 4-channel grid is small (above) or dim
+// is not a multiple of 4; CPL otherwise.
+FastShape bwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
+  FastShape sh = shape_of<BwdCfg>(x_dt);
+  if (W >= kBwdWideW) {
+    sh.cpl = cpl_wide(x_dt);
+  } else if (esize(x_dt) == 2 && B > 0 && T > 0 && D > 0) {
+    const Tiling t = bwd_tiling_for(B, T, D, sh.cpl, sh.nw);
+    if (D % sh.cpl || t.L < kBwdNarrowMinRows || B * t.nT * t.nGW < kTargetWaves)
+      sh.cpl = cpl_wide(x_dt);
+  }
+  return sh;
+}
+
+Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
+  const FastShape sh = bwd_shape(x_dt, B, T, D, W);
+  return bwd_tiling_for(B, T, D, sh.cpl, sh.nw);
 }
 
 Tiling generic_tiling(int64_t T) {
@@ -384,7 +413,7 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
     return fail(CCV1D_ERR_INVALID, "cannot take final-state gradients if seq_idx is given");
   if (D == 0) return CCV1D_OK;
   const bool empty = B == 0 || T == 0;
-  const int bcpl = bwd_shape(x_dtype, W).cpl;
+  const int bcpl = bwd_shape(x_dtype, B, T, D, W).cpl;
   const bool fast = !empty && fast_dtype(x_dtype, W) &&
                     rows_ok(x_dtype, bcpl, T, D, x, x_stride_b, x_stride_t) &&
                     rows_ok(x_dtype, bcpl, T, D, dout, dout_stride_b, dout_stride_t) &&

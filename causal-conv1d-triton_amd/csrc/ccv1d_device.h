@@ -21,6 +21,7 @@ struct Tiling {
   int32_t nGW;   // wave columns: ceil(D / VEC / 64)
   int32_t nTB;   // workgroups along time per batch row: ceil(nT / NW)
   int32_t nBlk;  // workgroups in the grid: B * nGW * nTB
+  int32_t vec;   // channels per lane the tiling was made for (0 for the generic kernels)
 };
 
 struct FwdParams {

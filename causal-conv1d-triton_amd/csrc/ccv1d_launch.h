@@ -95,34 +95,43 @@ static hipError_t fwd_one(const FwdParams& p, hipStream_t s) {
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
 }
 
-// Channels per lane of the backward for width W.
-template <typename TX, int W>
-constexpr int bwd_cpl() {
-  return W >= kBwdWideW ? BwdCfg<TX>::CPL_WIDE : BwdCfg<TX>::CPL;
-}
-
 // The backward's batch depth: C::R rows where the register budget holds it, else 2 rows, which
 // keeps the other instances from spilling. C::R fits at widths <= 4 with rows of at most 8 bytes
-// (4 waves per SIMD), and from kBwdWideW up with 16- and 8-bit types (2 channels per lane, 4-byte
-// rows: 88-104 VGPRs) except with seq_idx, whose kernel also holds the sequence ids. Measured
-// (fwd+bwd step, bf16, R = 4 against 2): B=4 T=8192 D=1024 W=6 -1.2 %, W=7 -2.8 %, W=8 -2.5 %;
-// B=8 T=4096 D=5376 W=8 -0.4 %; with seq_idx (B=4 T=16384 D=4096 W=7) +1 %, hence 2 there. Width 5
-// with 4 rows spills.
-template <typename TX, int W, bool SEQ>
+// (4 waves per SIMD), and with 2 channels of 16-bit x per lane (4-byte rows: 83-104 VGPRs at widths
+// 5-8) except with seq_idx from width 5, whose kernel also holds the sequence ids. Measured (fwd+bwd
+// step, bf16, R = 4 against 2): B=4 T=8192 D=1024 W=6 -1.2 %, W=7 -2.8 %, W=8 -2.5 %; B=8 T=4096
+// D=5376 W=8 -0.4 %; with seq_idx (B=4 T=16384 D=4096 W=7) +1 %, hence 2 there. Width 5 with 4
+// channels and 4 rows spills.
+template <typename TX, int W, bool SEQ, int CPL>
 constexpr int bwd_rows() {
   using C = BwdCfg<TX>;
-  if (W <= 4 && C::CPL * (int)sizeof(TX) <= 8) return C::R;
-  if (W >= kBwdWideW && !SEQ && C::CPL_WIDE * (int)sizeof(TX) <= 4) return C::R;
+  if (W <= 4 && CPL * (int)sizeof(TX) <= 8) return C::R;
+  if (!SEQ && CPL * (int)sizeof(TX) <= 4) return C::R;
   return 2;
 }
 
-template <typename TX, int W, bool SILU, bool SEQ>
+template <typename TX, int W, bool SILU, bool SEQ, int CPL>
 static hipError_t bwd_one(const BwdParams& p, hipStream_t s) {
   using C = BwdCfg<TX>;
   return launch(reinterpret_cast<const void*>(
-                    &bwd_fast_kernel<TX, W, SILU, SEQ, bwd_cpl<TX, W>(), C::NW,
-                                     bwd_rows<TX, W, SEQ>(), C::XLD, C::YLD, C::DXST>),
+                    &bwd_fast_kernel<TX, W, SILU, SEQ, CPL, C::NW, bwd_rows<TX, W, SEQ, CPL>(),
+                                     C::XLD, C::YLD, C::DXST>),
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
+}
+
+// The channels per lane the host's tiling chose (Tiling::vec): CPL_WIDE from kBwdWideW up; below
+// it CPL, or CPL_WIDE for 16-bit x. A tiling made for a width this build has no instance of is
+// rejected.
+template <typename TX, int W, bool SILU, bool SEQ>
+static hipError_t bwd_vec(const BwdParams& p, hipStream_t s) {
+  using C = BwdCfg<TX>;
+  if constexpr (W >= kBwdWideW || sizeof(TX) == 2) {
+    if (p.tl.vec == C::CPL_WIDE) return bwd_one<TX, W, SILU, SEQ, C::CPL_WIDE>(p, s);
+  }
+  if constexpr (W < kBwdWideW) {
+    if (p.tl.vec == C::CPL) return bwd_one<TX, W, SILU, SEQ, C::CPL>(p, s);
+  }
+  return hipErrorInvalidValue;
 }
 
 template <typename TX, int W>
@@ -135,8 +144,8 @@ static hipError_t fwd_w(const FwdParams& p, hipStream_t s) {
 template <typename TX, int W>
 static hipError_t bwd_w(const BwdParams& p, hipStream_t s) {
   const bool seq = p.seq != nullptr;
-  if (p.silu) return seq ? bwd_one<TX, W, true, true>(p, s) : bwd_one<TX, W, true, false>(p, s);
-  return seq ? bwd_one<TX, W, false, true>(p, s) : bwd_one<TX, W, false, false>(p, s);
+  if (p.silu) return seq ? bwd_vec<TX, W, true, true>(p, s) : bwd_vec<TX, W, true, false>(p, s);
+  return seq ? bwd_vec<TX, W, false, true>(p, s) : bwd_vec<TX, W, false, false>(p, s);
 }
 
 template <typename TX>
