@@ -21,6 +21,8 @@ namespace ccv1d {
 // and non-temporal stores their global-store path supports.
 template <typename TX> struct FwdCfg {
   static constexpr int CPL = 4;
+  // Small grids of 16-bit x: 2 channels per lane, twice the waves (chosen by the host per shape).
+  static constexpr int CPL_SMALL = 2;
   static constexpr int NW = 8;
   static constexpr int R = 4;
   static constexpr int XLD = kCachePlain;
@@ -87,12 +89,24 @@ hipError_t launch_fill(void* dst, int dst_dt, const void* src, int src_dt, int64
 
 namespace ccv1d {
 
-template <typename TX, int W, bool SILU, bool SEQ>
+template <typename TX, int W, bool SILU, bool SEQ, int CPL>
 static hipError_t fwd_one(const FwdParams& p, hipStream_t s) {
   using C = FwdCfg<TX>;
   return launch(reinterpret_cast<const void*>(
-                    &fwd_fast_kernel<TX, W, SILU, SEQ, C::CPL, C::NW, C::R, C::XLD, C::OST>),
+                    &fwd_fast_kernel<TX, W, SILU, SEQ, CPL, C::NW, C::R, C::XLD, C::OST>),
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
+}
+
+// The channels per lane the host's tiling chose (Tiling::vec): CPL, or CPL_SMALL for 16-bit x. A
+// tiling made for a width this build has no instance of is rejected.
+template <typename TX, int W, bool SILU, bool SEQ>
+static hipError_t fwd_vec(const FwdParams& p, hipStream_t s) {
+  using C = FwdCfg<TX>;
+  if constexpr (sizeof(TX) == 2) {
+    if (p.tl.vec == C::CPL_SMALL) return fwd_one<TX, W, SILU, SEQ, C::CPL_SMALL>(p, s);
+  }
+  if (p.tl.vec == C::CPL) return fwd_one<TX, W, SILU, SEQ, C::CPL>(p, s);
+  return hipErrorInvalidValue;
 }
 
 // The backward's batch depth: C::R rows where the register budget holds it, else 2 rows, which
@@ -137,8 +151,8 @@ static hipError_t bwd_vec(const BwdParams& p, hipStream_t s) {
 template <typename TX, int W>
 static hipError_t fwd_w(const FwdParams& p, hipStream_t s) {
   const bool seq = p.seq != nullptr;
-  if (p.silu) return seq ? fwd_one<TX, W, true, true>(p, s) : fwd_one<TX, W, true, false>(p, s);
-  return seq ? fwd_one<TX, W, false, true>(p, s) : fwd_one<TX, W, false, false>(p, s);
+  if (p.silu) return seq ? fwd_vec<TX, W, true, true>(p, s) : fwd_vec<TX, W, true, false>(p, s);
+  return seq ? fwd_vec<TX, W, false, true>(p, s) : fwd_vec<TX, W, false, false>(p, s);
 }
 
 template <typename TX, int W>
