@@ -550,6 +550,23 @@ def test_config2_readme_sweep(T, variant):
     compare(gpu, oracle_ref(inp, bias, cols=cols), bias, cols=cols)
 
 
+@pytest.mark.parametrize("B,T,D,W,xdt", [
+    (2, 8192, 1024, 4, torch.bfloat16),  # forward 4 channels per lane, backward 2 (small grid)
+    (4, 4096, 1024, 5, torch.float16),   # the same split at width 5 (backward with 4-row batches)
+    (4, 2048, 1002, 4, torch.bfloat16),  # dim not a multiple of 4: both passes 2 channels per lane
+    (1, 512, 262, 5, torch.float16),     # the same on a small grid at width 5
+    (4, 8192, 1024, 8, torch.bfloat16),  # width 8: 4-waves forward, 2-channel 4-row backward
+])
+def test_channels_per_lane_choices(B, T, D, W, xdt):
+    """Shapes on either side of the host's choice of 4 or 2 channels per lane in each pass, with
+    initial states, final states and their gradients, against the oracle on a channel subset."""
+    inp = make_inputs(B * T + D + W, B, T, D, W, xdt=xdt, init=True)
+    gpu = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=True)
+    cols = _cols(D, 40, B * T)
+    ref = oracle_ref(inp, True, cols=cols, final=True, dfinal=True, need_dinit=True)
+    compare(gpu, ref, True, cols=cols)
+
+
 def test_config3_mamba2_xbc():
     """B=8, T=4096, D=5376, W=4; x a channel slice of an in_proj output (time stride 10576)."""
     B, T, D, W = 8, 4096, 5376, 4
