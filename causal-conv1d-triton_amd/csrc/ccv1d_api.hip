@@ -130,18 +130,23 @@ Tiling fwd_tiling_for(int64_t B, int64_t T, int64_t D, int cpl, int nw) {
 }
 
 int fwd_cpl_small(int x_dt) {
-  return x_dt == CCV1D_BF16 ? FwdCfg<__bf16>::CPL_SMALL : FwdCfg<_Float16>::CPL_SMALL;
+  switch (x_dt) {
+    case CCV1D_BF16: return FwdCfg<__bf16>::CPL_SMALL;
+    case CCV1D_F16: return FwdCfg<_Float16>::CPL_SMALL;
+    default: return FwdCfg<float>::CPL_SMALL;
+  }
 }
 
-// Channels per lane and waves per workgroup of the vectorised forward for a shape: CPL, or for
-// 16-bit x CPL_SMALL when the CPL grid falls short of kTargetWaves waves even with its shortest
-// tiles (or dim is not a multiple of CPL). Measured (forward alone, bf16, W=4, 2 against 4
-// channels): B=4 D=1024 T=512 5.23 -> 4.68 us, T=2048 8.47 -> 8.11; B=16 D=2048 chunks of T=256
-// 9.36 -> 9.04 us per call, decode steps 2.56 -> 2.53. Grids that reach the target keep 4 channels
-// (benchmark shape 29.5 against 31.8 us; B=2 T=8192 D=1024 13.3 against 14.0).
+// Channels per lane and waves per workgroup of the vectorised forward for a shape: CPL, or
+// CPL_SMALL when the CPL grid falls short of kTargetWaves waves even with its shortest tiles (or
+// dim is not a multiple of CPL). Measured (forward alone, bf16, W=4, 2 against 4 channels): B=4
+// D=1024 T=512 5.23 -> 4.68 us, T=2048 8.47 -> 8.11; B=16 D=2048 chunks of T=256 9.36 -> 9.04 us
+// per call, decode steps 2.56 -> 2.53. Grids that reach the target keep 4 channels (benchmark shape
+// 29.5 against 31.8 us; B=2 T=8192 D=1024 13.3 against 14.0). fp32 x follows the same rule in both
+// passes (fwd+bwd step, B=4 D=1024 W=4: T=512 19.1 -> 16.8 us, T=2048 39.9 -> 37.7).
 FastShape fwd_shape(int x_dt, int64_t B, int64_t T, int64_t D) {
   FastShape sh = shape_of<FwdCfg>(x_dt);
-  if (esize(x_dt) == 2 && B > 0 && T > 0 && D > 0) {
+  if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
     const Tiling t = fwd_tiling_for(B, T, D, sh.cpl, sh.nw);
     if (D % sh.cpl || B * t.nT * t.nGW < kTargetWaves) sh.cpl = fwd_cpl_small(x_dt);
   }
@@ -167,8 +172,8 @@ Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int cpl, int nw) {
   return t;
 }
 
-// The vectorised backward of 16-bit x at widths under kBwdWideW takes 2 channels per lane instead
-// of 4 when the 4-channel grid is small: fewer than kTargetWaves waves, or tiles shortened below
+// The vectorised backward at widths under kBwdWideW takes 2 channels per lane instead of 4 when
+// the 4-channel grid is small: fewer than kTargetWaves waves, or tiles shortened below
 // kBwdNarrowMinRows rows to reach them. 2 channels per lane doubles the waves while keeping the
 // tiles longer. Measured (fwd+bwd step, bf16, 2 against 4 channels): B=4 D=1024 W=4 T=512 16.2 ->
 // 13.8 us, T=2048 24.1 -> 22.5, T=4096 39.9 -> 37.2; B=2 T=8192 D=1024 38.8 -> 36.8; W=2 T=512
@@ -187,13 +192,13 @@ int cpl_wide(int x_dt) {
 }
 
 // Channels per lane and waves per workgroup of the vectorised backward for a shape: CPL_WIDE from
-// kBwdWideW up (register budget), and for 16-bit x when the 4-channel grid is small (above) or dim
-// is not a multiple of 4; CPL otherwise.
+// kBwdWideW up (register budget), and below it when the 4-channel grid is small (above) or dim is
+// not a multiple of 4; CPL otherwise.
 FastShape bwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
   FastShape sh = shape_of<BwdCfg>(x_dt);
   if (W >= kBwdWideW) {
     sh.cpl = cpl_wide(x_dt);
-  } else if (esize(x_dt) == 2 && B > 0 && T > 0 && D > 0) {
+  } else if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
     const Tiling t = bwd_tiling_for(B, T, D, sh.cpl, sh.nw);
     if (D % sh.cpl || t.L < kBwdNarrowMinRows || B * t.nT * t.nGW < kTargetWaves)
       sh.cpl = cpl_wide(x_dt);

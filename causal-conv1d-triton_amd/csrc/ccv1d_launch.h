@@ -21,7 +21,7 @@ namespace ccv1d {
 // and non-temporal stores their global-store path supports.
 template <typename TX> struct FwdCfg {
   static constexpr int CPL = 4;
-  // Small grids of 16-bit x: 2 channels per lane, twice the waves (chosen by the host per shape).
+  // Small grids: 2 channels per lane, twice the waves (chosen by the host per shape).
   static constexpr int CPL_SMALL = 2;
   static constexpr int NW = 8;
   static constexpr int R = 4;
@@ -97,14 +97,12 @@ static hipError_t fwd_one(const FwdParams& p, hipStream_t s) {
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
 }
 
-// The channels per lane the host's tiling chose (Tiling::vec): CPL, or CPL_SMALL for 16-bit x. A
-// tiling made for a width this build has no instance of is rejected.
+// The channels per lane the host's tiling chose (Tiling::vec): CPL or CPL_SMALL. Any other value
+// is rejected.
 template <typename TX, int W, bool SILU, bool SEQ>
 static hipError_t fwd_vec(const FwdParams& p, hipStream_t s) {
   using C = FwdCfg<TX>;
-  if constexpr (sizeof(TX) == 2) {
-    if (p.tl.vec == C::CPL_SMALL) return fwd_one<TX, W, SILU, SEQ, C::CPL_SMALL>(p, s);
-  }
+  if (p.tl.vec == C::CPL_SMALL) return fwd_one<TX, W, SILU, SEQ, C::CPL_SMALL>(p, s);
   if (p.tl.vec == C::CPL) return fwd_one<TX, W, SILU, SEQ, C::CPL>(p, s);
   return hipErrorInvalidValue;
 }
@@ -134,14 +132,11 @@ static hipError_t bwd_one(const BwdParams& p, hipStream_t s) {
 }
 
 // The channels per lane the host's tiling chose (Tiling::vec): CPL_WIDE from kBwdWideW up; below
-// it CPL, or CPL_WIDE for 16-bit x. A tiling made for a width this build has no instance of is
-// rejected.
+// it CPL or CPL_WIDE. Any other value is rejected.
 template <typename TX, int W, bool SILU, bool SEQ>
 static hipError_t bwd_vec(const BwdParams& p, hipStream_t s) {
   using C = BwdCfg<TX>;
-  if constexpr (W >= kBwdWideW || sizeof(TX) == 2) {
-    if (p.tl.vec == C::CPL_WIDE) return bwd_one<TX, W, SILU, SEQ, C::CPL_WIDE>(p, s);
-  }
+  if (p.tl.vec == C::CPL_WIDE) return bwd_one<TX, W, SILU, SEQ, C::CPL_WIDE>(p, s);
   if constexpr (W < kBwdWideW) {
     if (p.tl.vec == C::CPL) return bwd_one<TX, W, SILU, SEQ, C::CPL>(p, s);
   }
