@@ -446,8 +446,9 @@ def main():
                     help="also run plain copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU; the op needs no collective (see DESIGN.md, "
-              "sharding). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this build measures one GPU; the op needs no collective (batch or "
+              "channel shards run the same kernels independently). Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
 
     from causal_conv1d_triton import causal_conv1d_fn
