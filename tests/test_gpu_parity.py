@@ -456,7 +456,7 @@ def _random_seq(g, B, T):
     return s
 
 
-@pytest.mark.parametrize("case", range(24))
+@pytest.mark.parametrize("case", range(48))
 def test_random_cases(case):
     """Random shapes, widths, dtypes and options (bias, activation, initial states, seq_idx with
     padding runs, final states with their gradient) against the oracle."""
