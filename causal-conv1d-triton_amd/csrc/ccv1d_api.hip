@@ -52,15 +52,20 @@ FastShape shape_of(int x_dt) {
 
 // Longest tile of the vectorised kernels (defaults and overrides alike). With seq_idx a wave reads the
 // ids of its tile and both halos (L + 2 (W - 1) rows) up front into one RowIds.
-// Every tile is at least kMinTileRows long (defaults and overrides), longer than any window (W - 1),
-// so only the first tile of a row has a window outside x.
+// Every tile is at least min_tile_rows(W) long (defaults and overrides), longer than the window
+// (W - 1), so only the first tile of a row has a window outside x.
 constexpr int kMaxTileRows = 64;
 constexpr int kMinTileRows = 8;
 static_assert(kMaxTileRows + 2 * (kMaxFastW - 1) <= kRowIds, "tile and halos must fit one RowIds");
-static_assert(kMinTileRows > kMaxFastW - 1, "a tile must be longer than the window");
+static_assert(kMinTileRows > kFwdWideW - 2 && 2 * kMinTileRows > kMaxFastW - 1,
+              "a tile must be longer than the window");
+
+// Shortest tile for width W: kMinTileRows, doubled from width kFwdWideW up.
+int min_tile_rows(int64_t W) { return W < kFwdWideW ? kMinTileRows : 2 * kMinTileRows; }
 
 // Row tiling overrides for tuning sweeps, read once: CCV1D_FWD_ROWS / CCV1D_BWD_ROWS (rows per tile
-// of the vectorised kernels; a power of two in [8, kMaxTileRows]).
+// of the vectorised kernels; a power of two in [8, kMaxTileRows], ignored for widths whose shortest
+// tile is longer).
 struct Tune {
   int fwd_rows = 0;
   int bwd_rows = 0;
@@ -122,10 +127,12 @@ Tiling fast_tiling(int64_t B, int64_t T, int64_t D, int vec, int nw, int lmin, i
 // D=1024 forward 7.0 -> 5.3 us; B=4 T=2048, whose 16-row grid has 256 workgroups, stays at 16).
 constexpr int64_t kFwdSmallGrid = 256;
 
-Tiling fwd_tiling_for(int64_t B, int64_t T, int64_t D, int cpl, int nw) {
-  Tiling t = fast_tiling(B, T, D, cpl, nw, 16, kMaxTileRows, kTargetWaves, tune().fwd_rows);
-  if (tune().fwd_rows == 0 && t.L == 16 && t.nBlk < kFwdSmallGrid)
-    t = fast_tiling(B, T, D, cpl, nw, kMinTileRows, kMinTileRows, kTargetWaves, kMinTileRows);
+Tiling fwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw) {
+  const int lmin = min_tile_rows(W);
+  const int over = tune().fwd_rows >= lmin ? tune().fwd_rows : 0;
+  Tiling t = fast_tiling(B, T, D, cpl, nw, 16, kMaxTileRows, kTargetWaves, over);
+  if (over == 0 && t.L == 16 && lmin < 16 && t.nBlk < kFwdSmallGrid)
+    t = fast_tiling(B, T, D, cpl, nw, lmin, lmin, kTargetWaves, lmin);
   return t;
 }
 
@@ -143,19 +150,22 @@ int fwd_cpl_small(int x_dt) {
 // D=1024 T=512 5.23 -> 4.68 us, T=2048 8.47 -> 8.11; B=16 D=2048 chunks of T=256 9.36 -> 9.04 us
 // per call, decode steps 2.56 -> 2.53. Grids that reach the target keep 4 channels (benchmark shape
 // 29.5 against 31.8 us; B=2 T=8192 D=1024 13.3 against 14.0). fp32 x follows the same rule in both
-// passes (fwd+bwd step, B=4 D=1024 W=4: T=512 19.1 -> 16.8 us, T=2048 39.9 -> 37.7).
-FastShape fwd_shape(int x_dt, int64_t B, int64_t T, int64_t D) {
+// passes (fwd+bwd step, B=4 D=1024 W=4: T=512 19.1 -> 16.8 us, T=2048 39.9 -> 37.7). From width
+// kFwdWideW up the forward always takes CPL_SMALL (its weights and window are per channel).
+FastShape fwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
   FastShape sh = shape_of<FwdCfg>(x_dt);
-  if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
-    const Tiling t = fwd_tiling_for(B, T, D, sh.cpl, sh.nw);
+  if (W >= kFwdWideW) {
+    sh.cpl = fwd_cpl_small(x_dt);
+  } else if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
+    const Tiling t = fwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);
     if (D % sh.cpl || B * t.nT * t.nGW < kTargetWaves) sh.cpl = fwd_cpl_small(x_dt);
   }
   return sh;
 }
 
-Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
-  const FastShape sh = fwd_shape(x_dt, B, T, D);
-  return fwd_tiling_for(B, T, D, sh.cpl, sh.nw);
+Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
+  const FastShape sh = fwd_shape(x_dt, B, T, D, W);
+  return fwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);
 }
 
 // Workgroups below which the backward halves its tiles (down to kMinTileRows): a grid with fewer
@@ -165,9 +175,11 @@ Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int x_dt) {
 // shape (512 workgroups) keeps 32 rows.
 constexpr int64_t kBwdSmallGrid = 256;
 
-Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int cpl, int nw) {
-  Tiling t = fast_tiling(B, T, D, cpl, nw, 32, kMaxTileRows, kTargetWaves, tune().bwd_rows);
-  while (tune().bwd_rows == 0 && t.nBlk < kBwdSmallGrid && t.L > kMinTileRows)
+Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw) {
+  const int lmin = min_tile_rows(W);
+  const int over = tune().bwd_rows >= lmin ? tune().bwd_rows : 0;
+  Tiling t = fast_tiling(B, T, D, cpl, nw, 32, kMaxTileRows, kTargetWaves, over);
+  while (over == 0 && t.nBlk < kBwdSmallGrid && t.L > lmin)
     t = fast_tiling(B, T, D, cpl, nw, t.L / 2, t.L / 2, kTargetWaves, t.L / 2);
   return t;
 }
@@ -199,7 +211,7 @@ FastShape bwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
   if (W >= kBwdWideW) {
     sh.cpl = cpl_wide(x_dt);
   } else if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
-    const Tiling t = bwd_tiling_for(B, T, D, sh.cpl, sh.nw);
+    const Tiling t = bwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);
     if (D % sh.cpl || t.L < kBwdNarrowMinRows || B * t.nT * t.nGW < kTargetWaves)
       sh.cpl = cpl_wide(x_dt);
   }
@@ -208,7 +220,7 @@ FastShape bwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
 
 Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
   const FastShape sh = bwd_shape(x_dt, B, T, D, W);
-  return bwd_tiling_for(B, T, D, sh.cpl, sh.nw);
+  return bwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);
 }
 
 Tiling generic_tiling(int64_t T) {
@@ -325,7 +337,7 @@ int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
     return fail(CCV1D_ERR_INVALID, "cannot return final states if seq_idx is given");
   if (B * T * D > 0 && !out) return fail(CCV1D_ERR_INVALID, "out is null");
   if (B * D == 0) return CCV1D_OK;
-  const int fcpl = fwd_shape(x_dtype, B, T, D).cpl;
+  const int fcpl = fwd_shape(x_dtype, B, T, D, W).cpl;
   const bool fast = T > 0 && fast_dtype(x_dtype, W) &&
                     rows_ok(x_dtype, fcpl, T, D, x, x_stride_b, x_stride_t) &&
                     rows_ok(x_dtype, fcpl, T, D, out, T * D, D) &&
@@ -333,7 +345,7 @@ int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   Tiling tl{};
   if (T > 0) {
     if (fast) {
-      tl = fwd_fast_tiling(B, T, D, x_dtype);
+      tl = fwd_fast_tiling(B, T, D, W, x_dtype);
     } else {
       if (W > kMaxGenericW) return fail(CCV1D_ERR_UNSUPPORTED, "width > %d", kMaxGenericW);
       tl = generic_tiling(T);

@@ -106,7 +106,7 @@ struct TileCoord {
 
 // Sequence ids of rows r0 .. r0 + 127 of concat(initial_states, x) (kRowIds rows), row r0 + j in
 // lane j of `lo` (j < 64) or lane j - 64 of `hi`, read with two vector loads issued together. A tile
-// and both its halos span at most 64 + 2 * 7 rows, so one RowIds serves every row a tile touches:
+// and both its halos span at most 64 + 2 * 15 rows, so one RowIds serves every row a tile touches:
 // at() gives the id of a row to the whole wave (v_readlane) without a load of its own, and no load
 // of ids then sits in the tile's pipelined loop, where its wait would also cover the loads and
 // stores issued before it.
@@ -355,13 +355,13 @@ __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBu
 // needs 132 otherwise, which leaves one 8-wave workgroup per CU (B=4 T=8192 D=1024 W=8 forward
 // 33.8 -> 31.4 us, B=8 T=4096 D=5376 W=8 150.6 -> 144.2 us; 2 VGPRs spill). Narrower widths already
 // fit; the seq_idx and fp32 instances would spill more, so they keep the default bound.
-template <typename TX, bool SEQ>
+template <typename TX, int W, bool SEQ>
 constexpr int fwd_waves_per_simd() {
-  return (sizeof(TX) == 2 && !SEQ) ? 4 : 2;
+  return (sizeof(TX) == 2 && !SEQ && W <= 8) ? 4 : 2;
 }
 
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int NW, int R, int XLD, int OST>
-__global__ __launch_bounds__(NW * 64, (fwd_waves_per_simd<TX, SEQ>())) void fwd_fast_kernel(
+__global__ __launch_bounds__(NW * 64, (fwd_waves_per_simd<TX, W, SEQ>())) void fwd_fast_kernel(
     const FwdParams p) {
   using IO = VecIO<TX, CPL>;
   constexpr int P = W - 1;

@@ -41,7 +41,8 @@ template <typename TX> struct BwdCfg {
   static constexpr int YLD = kCacheNT;
   static constexpr int DXST = sizeof(TX) == 2 ? kCacheSC1NT : kCacheNT;
 };
-constexpr int kMaxFastW = 8;     // widths 2..kMaxFastW have register-window kernels
+constexpr int kMaxFastW = 16;    // widths 2..kMaxFastW have register-window kernels
+constexpr int kFwdWideW = 9;     // first width whose forward always uses FwdCfg::CPL_SMALL
 constexpr int kBwdWideW = 6;     // first width whose backward uses BwdCfg::CPL_WIDE
 constexpr int kMaxGenericW = 128;  // LDS ring of the generic backward: 2 * W * 64 * 4 bytes
 constexpr int kReduceNW = 16;    // waves per reduction workgroup
@@ -97,13 +98,15 @@ static hipError_t fwd_one(const FwdParams& p, hipStream_t s) {
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
 }
 
-// The channels per lane the host's tiling chose (Tiling::vec): CPL or CPL_SMALL. Any other value
-// is rejected.
+// The channels per lane the host's tiling chose (Tiling::vec): CPL or CPL_SMALL below kFwdWideW,
+// CPL_SMALL from it. Any other value is rejected.
 template <typename TX, int W, bool SILU, bool SEQ>
 static hipError_t fwd_vec(const FwdParams& p, hipStream_t s) {
   using C = FwdCfg<TX>;
   if (p.tl.vec == C::CPL_SMALL) return fwd_one<TX, W, SILU, SEQ, C::CPL_SMALL>(p, s);
-  if (p.tl.vec == C::CPL) return fwd_one<TX, W, SILU, SEQ, C::CPL>(p, s);
+  if constexpr (W < kFwdWideW) {
+    if (p.tl.vec == C::CPL) return fwd_one<TX, W, SILU, SEQ, C::CPL>(p, s);
+  }
   return hipErrorInvalidValue;
 }
 
@@ -167,6 +170,14 @@ hipError_t launch_fwd_fast_t(const FwdParams& p, hipStream_t s) {
     case 6: return fwd_w<TX, 6>(p, s);
     case 7: return fwd_w<TX, 7>(p, s);
     case 8: return fwd_w<TX, 8>(p, s);
+    case 9: return fwd_w<TX, 9>(p, s);
+    case 10: return fwd_w<TX, 10>(p, s);
+    case 11: return fwd_w<TX, 11>(p, s);
+    case 12: return fwd_w<TX, 12>(p, s);
+    case 13: return fwd_w<TX, 13>(p, s);
+    case 14: return fwd_w<TX, 14>(p, s);
+    case 15: return fwd_w<TX, 15>(p, s);
+    case 16: return fwd_w<TX, 16>(p, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -181,6 +192,14 @@ hipError_t launch_bwd_fast_t(const BwdParams& p, hipStream_t s) {
     case 6: return bwd_w<TX, 6>(p, s);
     case 7: return bwd_w<TX, 7>(p, s);
     case 8: return bwd_w<TX, 8>(p, s);
+    case 9: return bwd_w<TX, 9>(p, s);
+    case 10: return bwd_w<TX, 10>(p, s);
+    case 11: return bwd_w<TX, 11>(p, s);
+    case 12: return bwd_w<TX, 12>(p, s);
+    case 13: return bwd_w<TX, 13>(p, s);
+    case 14: return bwd_w<TX, 14>(p, s);
+    case 15: return bwd_w<TX, 15>(p, s);
+    case 16: return bwd_w<TX, 16>(p, s);
     default: return hipErrorInvalidValue;
   }
 }

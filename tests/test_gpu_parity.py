@@ -181,9 +181,11 @@ def test_readme_example():
     compare(gpu, oracle_ref(inp, True), True)
 
 
-@pytest.mark.parametrize("W", [2, 3, 4, 5, 6, 7, 8, 9])
+@pytest.mark.parametrize("W", [2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 15, 16, 17, 24])
 @pytest.mark.parametrize("act", [None, "silu"])
 def test_widths_and_lengths(W, act):
+    """Widths of the register-window kernels (2-16) and of the generic ones (17, 24), at lengths
+    around the window (T = P - 1, P, P + 1) and beyond, with state handoff both ways."""
     P = W - 1
     for T in sorted({1, max(1, P - 1), P, P + 1, 17, 1000}):
         for D in (8, 1024):
@@ -465,7 +467,7 @@ def test_random_cases(case):
     B = pick([1, 2, 3, 4])
     T = pick([1, 2, 5, 9, 17, 64, 100, 333, 700])
     D = pick([8, 64, 100, 256, 264, 1000, 1024])
-    W = pick([2, 3, 4, 5, 6, 7, 8, 9])
+    W = pick([2, 3, 4, 5, 6, 7, 8, 9, 12, 16])
     xdt = pick([torch.bfloat16, torch.bfloat16, torch.float16, torch.float32])
     bias, silu, init = pick([True, False]), pick([True, False]), pick([True, False])
     seq = _random_seq(g, B, T) if pick([True, False]) else None
