@@ -282,7 +282,7 @@ def run_configs(dev, widths=False):
     call from replayed graphs after the usual warm-up, plus, for the latency-bound streaming and
     decode calls, the host-inclusive eager time per call. With `widths`, instead: the benchmark
     shape (bf16, bias + silu) at every width the vectorised kernels cover, forward alone and
-    forward + backward."""
+    forward + backward (widths 2-8, 9, 12 and 16)."""
     from causal_conv1d_triton import causal_conv1d_fn
     from causal_conv1d_triton.causal_conv1d import _fwd
 
@@ -335,7 +335,7 @@ def run_configs(dev, widths=False):
                  torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
                 for _ in range(4)]
         b = torch.randn(D, generator=gen, device=dev).requires_grad_(True)
-        for W in range(2, 9):
+        for W in (2, 3, 4, 5, 6, 7, 8, 9, 12, 16):
             w = (torch.randn(D, W, generator=gen, device=dev) / math.sqrt(W)).requires_grad_(True)
             fb, bb = _alg_bytes_general(B, T, D, W, True)
             shape = f"B={B} T={T} D={D} W={W} bias_silu"
@@ -441,7 +441,7 @@ def main():
     ap.add_argument("--configs", action="store_true",
                     help="instead of the headline line, one JSON line per BASELINE configuration 2-5")
     ap.add_argument("--widths", action="store_true",
-                    help="instead of the headline line, the benchmark shape at widths 2-8")
+                    help="instead of the headline line, the benchmark shape at widths 2-16")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
