@@ -4,5 +4,5 @@
 #include "ccv1d_launch.h"
 
 namespace ccv1d {
-template hipError_t launch_bwd_fast_t<_Float16>(const BwdParams& p, hipStream_t s);
+template hipError_t launch_bwd_fast_narrow_t<_Float16>(const BwdParams& p, hipStream_t s);
 }  // namespace ccv1d

@@ -4,5 +4,5 @@
 #include "ccv1d_launch.h"
 
 namespace ccv1d {
-template hipError_t launch_fwd_fast_t<float>(const FwdParams& p, hipStream_t s);
+template hipError_t launch_fwd_fast_narrow_t<float>(const FwdParams& p, hipStream_t s);
 }  // namespace ccv1d

@@ -72,10 +72,25 @@ inline hipError_t launch(const void* kernel, dim3 grid, dim3 block, size_t shmem
   return hipLaunchKernel(kernel, grid, block, args, shmem, s);
 }
 
+// The vectorised kernels of widths below kFwdWideW and of widths kFwdWideW..kMaxFastW are
+// instantiated in translation units of their own (ccv1d_{fwd,bwd}_<dtype>.hip and
+// ccv1d_{fwd,bwd}_<dtype>_wide.hip), so the build compiles them in parallel.
 template <typename TX>
-hipError_t launch_fwd_fast_t(const FwdParams& p, hipStream_t s);
+hipError_t launch_fwd_fast_narrow_t(const FwdParams& p, hipStream_t s);
 template <typename TX>
-hipError_t launch_bwd_fast_t(const BwdParams& p, hipStream_t s);
+hipError_t launch_fwd_fast_wide_t(const FwdParams& p, hipStream_t s);
+template <typename TX>
+hipError_t launch_bwd_fast_narrow_t(const BwdParams& p, hipStream_t s);
+template <typename TX>
+hipError_t launch_bwd_fast_wide_t(const BwdParams& p, hipStream_t s);
+template <typename TX>
+inline hipError_t launch_fwd_fast_t(const FwdParams& p, hipStream_t s) {
+  return p.W < kFwdWideW ? launch_fwd_fast_narrow_t<TX>(p, s) : launch_fwd_fast_wide_t<TX>(p, s);
+}
+template <typename TX>
+inline hipError_t launch_bwd_fast_t(const BwdParams& p, hipStream_t s) {
+  return p.W < kFwdWideW ? launch_bwd_fast_narrow_t<TX>(p, s) : launch_bwd_fast_wide_t<TX>(p, s);
+}
 template <typename TX>
 hipError_t launch_fwd_generic_t(const FwdParams& p, hipStream_t s);
 template <typename TX>
@@ -161,7 +176,7 @@ static hipError_t bwd_w(const BwdParams& p, hipStream_t s) {
 }
 
 template <typename TX>
-hipError_t launch_fwd_fast_t(const FwdParams& p, hipStream_t s) {
+hipError_t launch_fwd_fast_narrow_t(const FwdParams& p, hipStream_t s) {
   switch (p.W) {
     case 2: return fwd_w<TX, 2>(p, s);
     case 3: return fwd_w<TX, 3>(p, s);
@@ -170,6 +185,13 @@ hipError_t launch_fwd_fast_t(const FwdParams& p, hipStream_t s) {
     case 6: return fwd_w<TX, 6>(p, s);
     case 7: return fwd_w<TX, 7>(p, s);
     case 8: return fwd_w<TX, 8>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename TX>
+hipError_t launch_fwd_fast_wide_t(const FwdParams& p, hipStream_t s) {
+  switch (p.W) {
     case 9: return fwd_w<TX, 9>(p, s);
     case 10: return fwd_w<TX, 10>(p, s);
     case 11: return fwd_w<TX, 11>(p, s);
@@ -183,7 +205,7 @@ hipError_t launch_fwd_fast_t(const FwdParams& p, hipStream_t s) {
 }
 
 template <typename TX>
-hipError_t launch_bwd_fast_t(const BwdParams& p, hipStream_t s) {
+hipError_t launch_bwd_fast_narrow_t(const BwdParams& p, hipStream_t s) {
   switch (p.W) {
     case 2: return bwd_w<TX, 2>(p, s);
     case 3: return bwd_w<TX, 3>(p, s);
@@ -192,6 +214,13 @@ hipError_t launch_bwd_fast_t(const BwdParams& p, hipStream_t s) {
     case 6: return bwd_w<TX, 6>(p, s);
     case 7: return bwd_w<TX, 7>(p, s);
     case 8: return bwd_w<TX, 8>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename TX>
+hipError_t launch_bwd_fast_wide_t(const BwdParams& p, hipStream_t s) {
+  switch (p.W) {
     case 9: return bwd_w<TX, 9>(p, s);
     case 10: return bwd_w<TX, 10>(p, s);
     case 11: return bwd_w<TX, 11>(p, s);
