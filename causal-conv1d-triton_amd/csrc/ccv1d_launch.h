@@ -1,6 +1,7 @@
 // Launch helpers: compile-time configuration of the kernels and the dispatch from runtime
-// (width, activation, seq_idx) to template instantiations. Each x dtype's instantiations live in a
-// translation unit of their own (ccv1d_fast_<dtype>.hip) so they compile in parallel.
+// (width, activation, seq_idx, channels per lane) to template instantiations. Each pass, x dtype and
+// width range has its instantiations in a translation unit of its own
+// (ccv1d_{fwd,bwd}_<dtype>[_wide].hip), so they compile in parallel.
 #pragma once
 
 #include <hip/hip_ext.h>
