@@ -467,7 +467,7 @@ def test_random_cases(case):
     B = pick([1, 2, 3, 4])
     T = pick([1, 2, 5, 9, 17, 64, 100, 333, 700])
     D = pick([8, 64, 100, 256, 264, 1000, 1024])
-    W = pick([2, 3, 4, 5, 6, 7, 8, 9, 12, 16])
+    W = pick([2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 20])
     xdt = pick([torch.bfloat16, torch.bfloat16, torch.float16, torch.float32])
     bias, silu, init = pick([True, False]), pick([True, False]), pick([True, False])
     seq = _random_seq(g, B, T) if pick([True, False]) else None
