@@ -153,8 +153,9 @@ def bwd_workspace_bytes(B: int, T: int, D: int, W: int, x_dtype: torch.dtype) ->
     return load().ccv1d_bwd_workspace_bytes(B, T, D, W, DTYPE_CODES.get(x_dtype, 0))
 
 
-def bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit, dweight, dbias,
-        workspace, silu: bool) -> None:
+def _bwd_args(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit, dweight,
+              dbias, silu):
+    """Arguments of ccv1d_bwd before and after its (workspace, workspace_bytes) pair."""
     B, T, D = x.shape
     W = weight.shape[1]
     dev = x.get_device()
@@ -162,7 +163,7 @@ def bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit
         raise TypeError(f"dout dtype {dout.dtype} differs from x dtype {x.dtype}")
     if dfinal_states is not None and dfinal_states.dtype != x.dtype:
         raise TypeError(f"dfinal_states dtype {dfinal_states.dtype} differs from x dtype {x.dtype}")
-    args = (
+    head = (
         x.data_ptr(), x.stride(0), x.stride(1), _code(x),
         weight.data_ptr(), _code(weight),
         _ptr(bias), 0 if bias is None else _code(bias),
@@ -171,10 +172,15 @@ def bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit
         dout.data_ptr(), dout.stride(0), dout.stride(1),
         _ptr(dfinal_states),
         dx.data_ptr(), _ptr(dinit), dweight.data_ptr(), _ptr(dbias),
-        _ptr(workspace), 0 if workspace is None else workspace.numel(),
-        B, T, D, W,
-        int(silu), dev, _stream(dev),
     )
+    return head, (B, T, D, W, int(silu), dev, _stream(dev))
+
+
+def bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit, dweight, dbias,
+        workspace, silu: bool) -> None:
+    head, tail = _bwd_args(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit,
+                           dweight, dbias, silu)
+    args = head + (_ptr(workspace), 0 if workspace is None else workspace.numel()) + tail
     if _native is not None:
         rc = _native.bwd(*args)
     else:

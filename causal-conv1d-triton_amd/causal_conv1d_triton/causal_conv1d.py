@@ -20,9 +20,11 @@ from . import _ffi
 
 
 def _check_inputs(x, weight, bias, seq_idx, initial_states):
-    """Same assertions as the reference's _check_inputs (causal_conv1d.py:397-408). Each shape is
-    read once and devices are compared by index (x is on a GPU), which keeps the checks to about
-    1 us per call, a tenth of an eager decode step."""
+    """The reference's argument assertions (causal_conv1d.py:397-408), plus one it leaves to its
+    Triton launcher: every optional tensor must sit on x's GPU, since the library receives raw
+    device addresses and a host tensor's address would reach a kernel. Each shape is read once and
+    devices are compared by index (x is on a GPU), which keeps the checks to about 1 us per call, a
+    tenth of an eager decode step."""
     xs = x.shape
     assert len(xs) == 3, "x must be (batch, seqlen, dim)"
     B, T, D = xs
@@ -30,13 +32,30 @@ def _check_inputs(x, weight, bias, seq_idx, initial_states):
     assert len(ws) == 2 and ws[0] == D, "weight must be (dim, width)"
     W = ws[1]
     assert W >= 2, "width must be >= 2"
-    assert x.is_cuda and weight.get_device() == x.get_device()
-    assert bias is None or bias.shape == (D,)
-    assert initial_states is None or initial_states.shape == (B, W - 1, D)
-    assert seq_idx is None or seq_idx.shape == (B, T)
+    assert x.is_cuda, "x must be on a GPU"
+    dev = x.get_device()
+    assert weight.get_device() == dev, "weight must be on the device of x"
+    if bias is not None:
+        assert bias.shape == (D,), "bias must be (dim,)"
+        assert bias.get_device() == dev, "bias must be on the device of x"
+    if initial_states is not None:
+        assert initial_states.shape == (B, W - 1, D), "initial_states must be (batch, width - 1, dim)"
+        assert initial_states.get_device() == dev, "initial_states must be on the device of x"
+    if seq_idx is not None:
+        assert seq_idx.shape == (B, T), "seq_idx must be (batch, seqlen)"
+        assert seq_idx.get_device() == dev, "seq_idx must be on the device of x"
     # Offsets within one batch element are computed in int32.
     st = x.stride(1)
-    assert (T + W) * (st if st > D else D) < 2**31
+    assert (T + W) * (st if st > D else D) < 2**31, "seqlen * dim too large for 32-bit offsets"
+
+
+def _check_grads(x, dout, dfinal_states):
+    """The backward's incoming gradients must sit on x's device (the reference's launcher refuses
+    host tensors; here their addresses would reach a kernel)."""
+    dev = x.get_device()
+    assert dout.get_device() == dev, "the gradient of out must be on the device of x"
+    assert dfinal_states is None or dfinal_states.get_device() == dev, (
+        "the gradient of final_states must be on the device of x")
 
 
 def _channels_contiguous(t: Tensor) -> Tensor:
@@ -57,6 +76,7 @@ def _bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, need_din
     """Allocates the gradients and the fp32 partial-sum workspace and runs the backward kernels
     (reference `_bwd`, causal_conv1d.py:475-541). dweight and dbias are always computed; the
     empty-input cases (dweight = dbias = 0, dinit = dfinal) are handled inside the library."""
+    _check_grads(x, dout, dfinal_states)
     B, T, D = x.shape
     W = weight.shape[1]
     dx = torch.empty(B, T, D, device=x.device, dtype=x.dtype)
@@ -156,42 +176,51 @@ def _fwd_op_backward(ctx, dout, dfinal_states):
 _fwd_op.register_autograd(_fwd_op_backward, setup_context=_fwd_op_setup_context)
 
 
+def _new_final_states(x, width):
+    """Uninitialised (batch, width - 1, dim) buffer of x's dtype for the forward to fill."""
+    return torch.empty(x.shape[0], width - 1, x.shape[2], device=x.device, dtype=x.dtype)
+
+
 class _CausalConv1dFn(torch.autograd.Function):
-    """Autograd wiring of the reference (causal_conv1d.py:544-576): saves the inputs (not the
-    output) and recomputes the pre-activation in backward."""
+    """Eager autograd node (the reference's wiring, causal_conv1d.py:544-576). Only the inputs
+    are kept for the backward, never `out`: the backward kernel recomputes the pre-activation it
+    needs for silu, which costs arithmetic instead of a stored activation tensor."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, seq_idx, initial_states, return_final_states, silu):
-        final_states = None
-        if return_final_states:
-            final_states = torch.empty(
-                x.shape[0], weight.shape[1] - 1, x.shape[2], device=x.device, dtype=x.dtype
-            )
+        final_states = _new_final_states(x, weight.shape[1]) if return_final_states else None
         out = _fwd(x, weight, bias, seq_idx, initial_states, final_states, silu)
         ctx.save_for_backward(x, weight, bias, seq_idx, initial_states)
         ctx.silu = silu
         ctx.return_final_states = return_final_states
-        return (out, final_states) if return_final_states else out
+        if return_final_states:
+            return out, final_states
+        return out
 
     @staticmethod
-    def backward(ctx, dout, *args):
+    def backward(ctx, dout, *rest):
         x, weight, bias, seq_idx, initial_states = ctx.saved_tensors
-        dfinal_states = args[0] if ctx.return_final_states else None
-        if dfinal_states is not None:
-            dfinal_states = dfinal_states.contiguous()
-        need_dinit = initial_states is not None and ctx.needs_input_grad[4]
-        dx, dweight, dbias, dinit = _bwd(
-            x,
-            weight,
-            bias,
-            seq_idx,
-            initial_states,
-            _channels_contiguous(dout),
-            dfinal_states,
-            need_dinit,
-            ctx.silu,
-        )
+        # The final states' gradient exists only when they were returned (and autograd may still
+        # hand over None when they did not reach the loss).
+        dfinal = rest[0] if ctx.return_final_states and rest else None
+        if dfinal is not None:
+            dfinal = dfinal.contiguous()
+        want_dinit = initial_states is not None and ctx.needs_input_grad[4]
+        dx, dweight, dbias, dinit = _bwd(x, weight, bias, seq_idx, initial_states,
+                                         _channels_contiguous(dout), dfinal, want_dinit, ctx.silu)
+        # One gradient per forward input: x, weight, bias, seq_idx, initial_states and the two
+        # flags.
         return dx, dweight, dbias, None, dinit, None, None
+
+
+def _silu_flag(activation) -> bool:
+    """True for silu (also spelled swish), False for no activation; anything else is refused as
+    the reference refuses it (causal_conv1d.py:605-606)."""
+    if activation is None:
+        return False
+    if activation == "silu" or activation == "swish":
+        return True
+    raise NotImplementedError("activation must be None, silu, or swish")
 
 
 def causal_conv1d_fn(
@@ -204,59 +233,69 @@ def causal_conv1d_fn(
     final_states_out: Tensor | None = None,
     activation: str | None = None,
 ) -> Tensor | tuple[Tensor, Tensor]:
-    """Causal depthwise conv1d over channels-last inputs (reference causal_conv1d.py:579-639).
+    """Depthwise causal convolution along time, with autograd (interface of the reference's
+    causal_conv1d.py:579-639).
 
-    x: (batch, seqlen, dim); must be contiguous along dim
-    weight: (dim, width), width >= 2
-    bias: (dim,)
-    seq_idx: (batch, seqlen) integer sequence ids for packed sequences. Positions with negative ids
-        are considered padding, and give zero outputs. Can be combined with initial_states, which
-        count as part of seq_idx[:, 0]'s sequence, but cannot be combined with return_final_states
-    initial_states: (batch, width - 1, dim), the inputs preceding x[:, 0]
-    return_final_states: also return the last width - 1 rows of concat(initial_states, x), i.e. the
-        initial_states for continuing the sequence; supports grad
-    final_states_out: optional (batch, width - 1, dim) buffer to copy the final states into
-    activation: None, "silu", or "swish"
+    Each channel d of x has its own filter weight[d, :] of length W; output row t sees input rows
+    t-W+1 .. t, and rows before the start come from `initial_states` (zeros when it is None):
 
-    Returns out of shape (batch, seqlen, dim) and dtype x.dtype, or (out, final_states).
+        out[b, t, d] = act(bias[d] + sum_{k<W} weight[d, k] * xx[b, t - W + 1 + k, d])
+        xx = cat(initial_states, x) along time
+
+    Arguments:
+      x: (batch, seqlen, dim) on a GPU, fp32/fp16/bf16, unit stride along dim (other strides are
+         free; a tensor without one is copied first).
+      weight: (dim, width) with width >= 2, any float dtype; dweight comes back in that dtype.
+      bias: optional (dim,).
+      seq_idx: optional (batch, seqlen) integer ids marking packed sequences: a tap only reaches
+         rows with the same id as the output row, and rows with a negative id are padding, whose
+         outputs (and input gradients) are zero. initial_states are treated as rows of
+         seq_idx[:, 0]'s sequence. Not allowed together with return_final_states.
+      initial_states: optional (batch, width - 1, dim), the width - 1 rows that precede x[:, 0].
+      return_final_states: also return the last width - 1 rows of cat(initial_states, x), which
+         are the initial_states of a following chunk; gradients flow through them.
+      final_states_out: optional (batch, width - 1, dim) tensor that receives a copy of the final
+         states and is returned in their place; needs return_final_states=True.
+      activation: None, or "silu" (same as "swish").
+
+    Returns `out` (batch, seqlen, dim) in x's dtype, or `(out, final_states)`. All arithmetic is
+    fp32; the kernels are the HIP kernels of libccv1d.so, with no other compute path.
     """
-    if activation not in (None, "silu", "swish"):
-        raise NotImplementedError("activation must be None, silu, or swish")
+    silu = _silu_flag(activation)
     if seq_idx is not None:
         assert not return_final_states, "cannot return final states if seq_idx is not None"
     if final_states_out is not None:
         assert return_final_states, "final_states_out requires return_final_states=True"
     _check_inputs(x, weight, bias, seq_idx, initial_states)
-
     x = _channels_contiguous(x)
     weight = weight.contiguous()
-    bias = bias.contiguous() if bias is not None else None
-    seq_idx = seq_idx.to(torch.int32).contiguous() if seq_idx is not None else None
-    initial_states = initial_states.contiguous() if initial_states is not None else None
-    silu = activation is not None
+    if bias is not None:
+        bias = bias.contiguous()
+    if seq_idx is not None:
+        seq_idx = seq_idx.to(torch.int32).contiguous()
+    if initial_states is not None:
+        initial_states = initial_states.contiguous()
 
-    needs_grad = torch.is_grad_enabled() and any(
-        t is not None and t.requires_grad for t in (x, weight, bias, initial_states)
-    )
+    final_states = None
     if torch.compiler.is_compiling():
-        # Under torch.compile the passes go through the registered custom operators.
-        out, final_states = _fwd_op(x, weight, bias, seq_idx, initial_states, return_final_states,
-                                    silu)
-        result = (out, final_states) if return_final_states else out
-    elif needs_grad:
-        result = _CausalConv1dFn.apply(
-            x, weight, bias, seq_idx, initial_states, return_final_states, silu
-        )
+        # Traced by torch.compile: the registered operators carry the passes and their autograd.
+        out, final_states = _fwd_op(x, weight, bias, seq_idx, initial_states,
+                                    return_final_states, silu)
+    elif torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad
+                                      or (bias is not None and bias.requires_grad)
+                                      or (initial_states is not None
+                                          and initial_states.requires_grad)):
+        res = _CausalConv1dFn.apply(x, weight, bias, seq_idx, initial_states,
+                                    return_final_states, silu)
+        out, final_states = res if return_final_states else (res, None)
     else:
-        final_states = None
+        # Inference: no autograd node, the forward kernel writes straight into fresh buffers.
         if return_final_states:
-            final_states = torch.empty(
-                x.shape[0], weight.shape[1] - 1, x.shape[2], device=x.device, dtype=x.dtype
-            )
+            final_states = _new_final_states(x, weight.shape[1])
         out = _fwd(x, weight, bias, seq_idx, initial_states, final_states, silu)
-        result = (out, final_states) if return_final_states else out
 
+    if not return_final_states:
+        return out
     if final_states_out is not None:
-        out, final_states = result
-        result = out, final_states_out.copy_(final_states)
-    return result
+        final_states = final_states_out.copy_(final_states)
+    return out, final_states

@@ -63,15 +63,19 @@ static_assert(kMinTileRows > kFwdWideW - 2 && 2 * kMinTileRows > kMaxFastW - 1,
 // Shortest tile for width W: kMinTileRows, doubled from width kFwdWideW up.
 int min_tile_rows(int64_t W) { return W < kFwdWideW ? kMinTileRows : 2 * kMinTileRows; }
 
-// Row tiling overrides for tuning sweeps, read once: CCV1D_FWD_ROWS / CCV1D_BWD_ROWS (rows per tile
-// of the vectorised kernels; a power of two in [8, kMaxTileRows], ignored for widths whose shortest
-// tile is longer).
+// Row tiling overrides for tuning sweeps: CCV1D_FWD_ROWS / CCV1D_BWD_ROWS (rows per tile of the
+// vectorised kernels; a power of two in [8, kMaxTileRows], ignored for widths whose shortest tile
+// is longer). They change the backward's partial-row count and hence the dweight/dbias summation
+// order, so they exist only in a library built with -DCCV1D_TUNING (make EXTRA_HIPFLAGS=
+// -DCCV1D_TUNING); the shipped library ignores the environment and its tiling depends on the
+// shape alone.
 struct Tune {
   int fwd_rows = 0;
   int bwd_rows = 0;
 };
 
 const Tune& tune() {
+#ifdef CCV1D_TUNING
   static const Tune t = [] {
     Tune v;
     auto rd = [](const char* name) {
@@ -84,6 +88,9 @@ const Tune& tune() {
     v.bwd_rows = rd("CCV1D_BWD_ROWS");
     return v;
   }();
+#else
+  static const Tune t{};
+#endif
   return t;
 }
 
@@ -427,16 +434,33 @@ size_t ccv1d_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t dim, int
   return (size_t)(rows * (W + 1) * D * (int64_t)sizeof(float));
 }
 
-int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
-              const void* weight, int weight_dtype, const void* bias, int bias_dtype,
-              const int32_t* seq_idx, const void* initial_states, int init_dtype,
-              const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
-              const void* dfinal_states, void* dx, void* dinitial_states, void* dweight,
-              void* dbias, void* workspace, size_t workspace_bytes, int64_t batch, int64_t seqlen,
-              int64_t dim, int64_t width, int silu, int device, void* stream) {
-  g_last_error.clear();
-  const bool timed = take_timing_request();
-  const int64_t B = batch, T = seqlen, D = dim, W = width, P = W - 1;
+}  // extern "C"
+
+namespace {
+
+// A validated backward request: the kernel parameters, the path, the tiling and the workspace it
+// needs, with everything but the workspace address filled in. Planning makes no HIP call, so a
+// request is refused (status and message) before anything touches a device.
+struct BwdPlan {
+  BwdParams p{};
+  ReduceParams r{};
+  bool skip = false;   // dim == 0: nothing to do
+  bool empty = false;  // batch == 0 or seqlen == 0: the fill path
+  bool fast = false;
+  int x_dt = 0;
+  size_t need = 0;     // workspace bytes the launches use
+};
+
+// `ws_aligned`: the workspace the call will use is 16-byte aligned (the vectorised backward stores
+// partial rows with 16-byte accesses).
+int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+             const void* weight, int weight_dtype, const void* bias, int bias_dtype,
+             const int32_t* seq_idx, const void* initial_states, int init_dtype,
+             const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
+             const void* dfinal_states, void* dx, void* dinitial_states, void* dweight,
+             void* dbias, bool ws_aligned, int64_t batch, int64_t seqlen, int64_t dim,
+             int64_t width, int silu, BwdPlan& pl) {
+  const int64_t B = batch, T = seqlen, D = dim, W = width;
   int rc = check_common(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
                         initial_states, init_dtype, B, T, D, W);
   if (rc) return rc;
@@ -451,49 +475,11 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
     return fail(CCV1D_ERR_INVALID, "dinitial_states requires initial_states");
   if (seq_idx && dfinal_states)
     return fail(CCV1D_ERR_INVALID, "cannot take final-state gradients if seq_idx is given");
-  if (D == 0) return CCV1D_OK;
-  const bool empty = B == 0 || T == 0;
-  const int bcpl = bwd_shape(x_dtype, B, T, D, W).cpl;
-  const bool fast = !empty && fast_dtype(x_dtype, W) &&
-                    rows_ok(x_dtype, bcpl, T, D, x, x_stride_b, x_stride_t) &&
-                    rows_ok(x_dtype, bcpl, T, D, dout, dout_stride_b, dout_stride_t) &&
-                    rows_ok(x_dtype, bcpl, T, D, dx, T * D, D) &&
-                    (!dfinal_states || aligned_to(dfinal_states, bcpl * esize(x_dtype))) &&
-                    aligned_to(workspace, 16);
-  Tiling tl{};
-  int64_t rows = 0;
-  if (!empty) {
-    if (fast) {
-      tl = bwd_fast_tiling(B, T, D, W, x_dtype);
-      rows = B * tl.nTB;
-    } else {
-      if (W > kMaxGenericW) return fail(CCV1D_ERR_UNSUPPORTED, "width > %d", kMaxGenericW);
-      tl = generic_tiling(T);
-      rows = B * tl.nT;
-      if (rows >= (int64_t(1) << 31) || cdiv(D, 64) > 65535)
-        return fail(CCV1D_ERR_UNSUPPORTED, "shape too large for the generic kernel");
-    }
-    const size_t need = (size_t)(rows * (W + 1) * D * (int64_t)sizeof(float));
-    if (!workspace || workspace_bytes < need)
-      return fail(CCV1D_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes,
-                  need);
-  }
-  DeviceGuard guard(device);
-  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  pl.x_dt = x_dtype;
+  pl.skip = D == 0;
+  pl.empty = B == 0 || T == 0;
 
-  if (empty) {
-    // No outputs: dweight = dbias = 0, and the initial-state gradient is the final-state gradient
-    // (causal_conv1d.py:480-489).
-    hipError_t e = launch_fill(dweight, weight_dtype, nullptr, 0, D * W, s);
-    if (e == hipSuccess && dbias) e = launch_fill(dbias, bias_dtype, nullptr, 0, D, s);
-    if (e == hipSuccess && dinitial_states)
-      e = launch_fill(dinitial_states, init_dtype, dfinal_states, x_dtype, B * P * D, s);
-    if (e != hipSuccess) return hip_fail(e, "fill launch");
-    return CCV1D_OK;
-  }
-
-  BwdParams p{};
+  BwdParams& p = pl.p;
   p.x = x;
   p.w = weight;
   p.bias = bias;
@@ -503,7 +489,6 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   p.dfin = dfinal_states;
   p.dx = dx;
   p.dinit = dinitial_states;
-  p.part = static_cast<float*>(workspace);
   p.s_xb = x_stride_b;
   p.s_yb = dout_stride_b;
   p.s_xt = (int32_t)x_stride_t;
@@ -520,24 +505,74 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   p.has_dfinal = dfinal_states != nullptr;
   p.need_dinit = dinitial_states != nullptr;
   p.silu = silu != 0;
-  if (fast) {
+  ReduceParams& r = pl.r;
+  r.dw = dweight;
+  r.db = dbias;
+  r.D = (int32_t)D;
+  r.W = (int32_t)W;
+  r.w_dt = weight_dtype;
+  r.b_dt = bias_dtype;
+  r.has_bias = bias != nullptr;
+  if (pl.skip || pl.empty) return CCV1D_OK;
+
+  const int bcpl = bwd_shape(x_dtype, B, T, D, W).cpl;
+  pl.fast = fast_dtype(x_dtype, W) && rows_ok(x_dtype, bcpl, T, D, x, x_stride_b, x_stride_t) &&
+            rows_ok(x_dtype, bcpl, T, D, dout, dout_stride_b, dout_stride_t) &&
+            rows_ok(x_dtype, bcpl, T, D, dx, T * D, D) &&
+            (!dfinal_states || aligned_to(dfinal_states, bcpl * esize(x_dtype))) && ws_aligned;
+  int64_t rows;
+  if (pl.fast) {
+    p.tl = bwd_fast_tiling(B, T, D, W, x_dtype);
+    rows = B * p.tl.nTB;
     p.x_bytes = slab_bytes(x_dtype, T, D, x_stride_t);
     p.y_bytes = slab_bytes(x_dtype, T, D, dout_stride_t);
     p.o_bytes = slab_bytes(x_dtype, T, D, D);
+  } else {
+    if (W > kMaxGenericW) return fail(CCV1D_ERR_UNSUPPORTED, "width > %d", kMaxGenericW);
+    p.tl = generic_tiling(T);
+    rows = B * p.tl.nT;
+    if (rows >= (int64_t(1) << 31) || cdiv(D, 64) > 65535)
+      return fail(CCV1D_ERR_UNSUPPORTED, "shape too large for the generic kernel");
+  }
+  r.Pn = (int32_t)rows;
+  pl.need = (size_t)(rows * (W + 1) * D * (int64_t)sizeof(float));
+  return CCV1D_OK;
+}
+
+// Launches a planned backward with `workspace` (at least pl.need bytes) on `stream`: the main
+// kernel then the reduction, or the fills of the empty path.
+int run_bwd(BwdPlan& pl, void* workspace, int device, void* stream, bool timed) {
+  if (pl.skip) return CCV1D_OK;
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const BwdParams& p = pl.p;
+
+  if (pl.empty) {
+    // No outputs: dweight = dbias = 0, and the initial-state gradient is the final-state gradient
+    // (causal_conv1d.py:480-489).
+    const int64_t P = p.W - 1;
+    hipError_t e = launch_fill(pl.r.dw, p.w_dt, nullptr, 0, (int64_t)p.D * p.W, s);
+    if (e == hipSuccess && pl.r.db) e = launch_fill(pl.r.db, p.b_dt, nullptr, 0, p.D, s);
+    if (e == hipSuccess && p.dinit)
+      e = launch_fill(p.dinit, p.i_dt, p.dfin, pl.x_dt, (int64_t)p.B * P * p.D, s);
+    if (e != hipSuccess) return hip_fail(e, "fill launch");
+    return CCV1D_OK;
   }
 
-  p.tl = tl;
+  pl.p.part = static_cast<float*>(workspace);
+  pl.r.part = pl.p.part;
   hipError_t e;
   {
     const TimedLaunch timing(timed);
-    if (fast) {
-      switch (x_dtype) {
+    if (pl.fast) {
+      switch (pl.x_dt) {
         case CCV1D_BF16: e = launch_bwd_fast_t<__bf16>(p, s); break;
         case CCV1D_F16: e = launch_bwd_fast_t<_Float16>(p, s); break;
         default: e = launch_bwd_fast_t<float>(p, s); break;
       }
     } else {
-      switch (x_dtype) {
+      switch (pl.x_dt) {
         case CCV1D_BF16: e = launch_bwd_generic_t<__bf16>(p, s); break;
         case CCV1D_F16: e = launch_bwd_generic_t<_Float16>(p, s); break;
         case CCV1D_F32: e = launch_bwd_generic_t<float>(p, s); break;
@@ -546,20 +581,34 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
     }
   }
   if (e != hipSuccess) return hip_fail(e, "backward launch");
-
-  ReduceParams r{};
-  r.part = p.part;
-  r.dw = dweight;
-  r.db = dbias;
-  r.Pn = (int32_t)rows;
-  r.D = (int32_t)D;
-  r.W = (int32_t)W;
-  r.w_dt = weight_dtype;
-  r.b_dt = bias_dtype;
-  r.has_bias = bias != nullptr;
-  e = launch_reduce(r, s);
+  e = launch_reduce(pl.r, s);
   if (e != hipSuccess) return hip_fail(e, "reduce launch");
   return CCV1D_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+              const void* weight, int weight_dtype, const void* bias, int bias_dtype,
+              const int32_t* seq_idx, const void* initial_states, int init_dtype,
+              const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
+              const void* dfinal_states, void* dx, void* dinitial_states, void* dweight,
+              void* dbias, void* workspace, size_t workspace_bytes, int64_t batch, int64_t seqlen,
+              int64_t dim, int64_t width, int silu, int device, void* stream) {
+  g_last_error.clear();
+  const bool timed = take_timing_request();
+  BwdPlan pl;
+  int rc = plan_bwd(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
+                    seq_idx, initial_states, init_dtype, dout, dout_stride_b, dout_stride_t,
+                    dfinal_states, dx, dinitial_states, dweight, dbias, aligned_to(workspace, 16),
+                    batch, seqlen, dim, width, silu, pl);
+  if (rc) return rc;
+  if (pl.need > 0 && (!workspace || workspace_bytes < pl.need))
+    return fail(CCV1D_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes,
+                pl.need);
+  return run_bwd(pl, workspace, device, stream, timed);
 }
 
 }  // extern "C"

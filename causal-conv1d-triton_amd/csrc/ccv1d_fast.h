@@ -1,5 +1,5 @@
-// Vectorised forward and backward kernels for compile-time widths (2..8) and channels-last x whose
-// rows are 8- or 16-byte aligned.
+// Vectorised forward and backward kernels for compile-time widths (2..kMaxFastW = 16) and
+// channels-last x whose rows are aligned to the 4-, 8- or 16-byte access of CPL channels.
 //
 // Work decomposition (both passes): a lane owns CPL consecutive channels, a wave owns 64 such
 // channel vectors over a tile of L consecutive rows, and a workgroup holds NW waves on consecutive
@@ -248,8 +248,9 @@ __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBu
 
   FwdLane<TX, W, SILU, SEQ, CPL> s;
   load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
-  // Tiles are at least 8 rows long, so a tile starts at row 0 or at a row >= 8 > P: a window not in
-  // x is the first tile's, the P initial-state rows (or zeros).
+  // Every tile is at least min_tile_rows(W) > P rows long (the host's tiling; static_assert in
+  // ccv1d_api.hip), so a tile starts at row 0 or at a row >= P: a window not in x is the first
+  // tile's, the P initial-state rows (or zeros).
   if (halo_in_x) {
 #pragma unroll
     for (int k = 0; k < P; ++k) IO::unpack(hr[k], s.xw[k]);
@@ -288,8 +289,8 @@ __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBu
   }
 }
 
-// One tile walked backward (outputs t1-1 down to t0), for tiles with t0 >= 8 > P, whose rows all
-// lie in x. The window starts as rows t1-1-P .. t1-1; output t then takes in row t-P-1. Rows below
+// One tile walked backward (outputs t1-1 down to t0), for tiles with t0 >= min_tile_rows(W) > P,
+// whose rows all lie in x. The window starts as rows t1-1-P .. t1-1; output t then takes in row t-P-1. Rows below
 // t0-P are clamped to t0-P, for the same reason as the clamp of the forward walk.
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int R, int XLD, int OST>
 __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBuf<TX, CPL, XLD>& X,
@@ -624,8 +625,9 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
     }
     load(Ax, Ay, t_main);
     load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
-    // Tiles are at least 8 rows long, so a tile starts at row 0 or at a row >= 8 > P: a window not
-    // in x is the first tile's, the P initial-state rows (or zeros).
+    // Every tile is at least min_tile_rows(W) > P rows long (the host's tiling; static_assert in
+    // ccv1d_api.hip), so a tile starts at row 0 or at a row >= P: a window not in x is the first
+    // tile's, the P initial-state rows (or zeros).
     if (halo_in_x) {
 #pragma unroll
       for (int k = 0; k < P; ++k) IO::unpack(hr[k], s.xw[k]);

@@ -1,5 +1,6 @@
-// Scalar kernels for what the vectorised path does not cover: widths above 8, channel counts that
-// are not a multiple of the 16-byte vector, rows that are not 16-byte aligned, and fp64 x. One lane
+// Scalar kernels for what the vectorised path does not cover: widths above kMaxFastW (16), channel
+// counts that are not a multiple of the channels per lane, rows not aligned to the vector access,
+// and fp64 x. One lane
 // owns one channel of one tile; the lanes of a wave cover 64 consecutive channels, so every row
 // access is still coalesced. Also: the deterministic partial-sum reduction and the small fill/copy
 // kernel used by the empty-sequence paths.

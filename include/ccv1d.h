@@ -24,7 +24,8 @@
  *    for dout must be below 2^31.
  *  - Return value: CCV1D_OK (0) or an error code; ccv1d_last_error() then describes the failure.
  *  - Reentrant and thread-safe; the only global state is the error string and the timing request of
- *    ccv1d_time_main_kernel (both thread-local) and a tuning table read once from the environment.
+ *    ccv1d_time_main_kernel (both thread-local). The library reads nothing from the environment:
+ *    its tiling, and with it every summation order, is a function of the shape alone.
  */
 #ifndef CCV1D_H
 #define CCV1D_H

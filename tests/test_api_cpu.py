@@ -105,3 +105,47 @@ def test_custom_op_fake_shapes(bias, init, final):
         assert dw.shape == w.shape and dw.dtype == w.dtype
         assert db.shape == ((D,) if bias else (0,)) and (not bias or db.dtype == b.dtype)
         assert di.shape == ((B, W - 1, D) if init else (0,)) and (not init or di.dtype == s0.dtype)
+
+
+@pytest.mark.parametrize("which", ["weight", "bias", "initial_states", "seq_idx"])
+def test_host_tensors_rejected_before_launch(which):
+    """Every optional tensor must be on x's GPU: the library takes raw device addresses, so a host
+    tensor is refused with an AssertionError (as the reference refuses a host weight,
+    causal_conv1d.py:403) before anything is launched. Fake CUDA tensors stand in for the GPU, and
+    the tensor under test is a real host tensor."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    B, T, D, W = 2, 16, 8, 4
+    host = {
+        "weight": torch.randn(D, W),
+        "bias": torch.randn(D),
+        "initial_states": torch.randn(B, W - 1, D),
+        "seq_idx": torch.zeros(B, T, dtype=torch.int32),
+    }[which]
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        x = torch.empty(B, T, D, device="cuda", dtype=torch.bfloat16)
+        kw = {"weight": torch.empty(D, W, device="cuda")}
+        kw[which] = host
+        with pytest.raises(AssertionError, match="device of x"):
+            causal_conv1d_fn(x, **kw)
+
+
+@pytest.mark.parametrize("which", ["dout", "dfinal_states"])
+def test_host_gradients_rejected_before_launch(which):
+    """The backward entry refuses incoming gradients that are not on x's device."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from causal_conv1d_triton.causal_conv1d import _bwd
+
+    B, T, D, W = 2, 16, 8, 4
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        x = torch.empty(B, T, D, device="cuda", dtype=torch.bfloat16)
+        w = torch.empty(D, W, device="cuda")
+        dout = torch.empty(B, T, D, device="cuda", dtype=torch.bfloat16)
+        dfin = torch.empty(B, W - 1, D, device="cuda", dtype=torch.bfloat16)
+        if which == "dout":
+            dout = torch.randn(B, T, D).to(torch.bfloat16)
+        else:
+            dfin = torch.randn(B, W - 1, D).to(torch.bfloat16)
+        with pytest.raises(AssertionError, match="device of x"):
+            _bwd(x, w, None, None, None, dout, dfin, False, True)
