@@ -83,6 +83,9 @@ def load() -> ctypes.CDLL:
         _c_i64, _c_i64, _c_i64, _c_i64,  # batch, seqlen, dim, width
         _c_int, _c_int, _c_ptr,  # silu, device, stream
     ]
+    lib.ccv1d_bwd_noalloc.restype = _c_int
+    lib.ccv1d_bwd_noalloc.argtypes = (lib.ccv1d_bwd.argtypes[:19]   # x .. dbias, as ccv1d_bwd
+                                      + lib.ccv1d_bwd.argtypes[21:])  # batch .. stream
     _lib = lib
     return lib
 
@@ -174,6 +177,16 @@ def _bwd_args(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx,
         dx.data_ptr(), _ptr(dinit), dweight.data_ptr(), _ptr(dbias),
     )
     return head, (B, T, D, W, int(silu), dev, _stream(dev))
+
+
+def bwd_noalloc(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit, dweight,
+                dbias, silu: bool) -> None:
+    """ccv1d_bwd_noalloc through ctypes: the backward with the library's built-in scratch instead
+    of a workspace (for callers that cannot allocate)."""
+    head, tail = _bwd_args(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit,
+                           dweight, dbias, silu)
+    lib = load()
+    _check(lib.ccv1d_bwd_noalloc(*head, *tail), lib)
 
 
 def bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit, dweight, dbias,

@@ -2,9 +2,11 @@
 // the choice between the vectorised and the generic kernels, time tiling, and launches on the
 // caller's stream. This is the host launcher layer of the reference (`_fwd`, `_bwd`, `_chunking`;
 // causal_conv1d.py:377-541) moved into native code.
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include "ccv1d.h"
@@ -438,6 +440,38 @@ size_t ccv1d_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t dim, int
 
 namespace {
 
+// Scratch of the allocation-free backward (ccv1d_bwd_noalloc): its fp32 partial rows live here
+// instead of in a caller workspace. The name is a host-side stand-in; the device address comes
+// from hipGetSymbolAddress (scratch_on_current_device), once per device, and only that address is
+// ever given to kernels. Every device the library runs on holds its own copy until the process
+// ends.
+static __device__ __align__(256) unsigned char scratch[CCV1D_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on `device`, which must be the current device. Resolved at the
+// first call on each device and kept.
+int scratch_on_current_device(int device, void** addr) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(CCV1D_ERR_INVALID, "device %d outside the %d devices the scratch table covers",
+                device, kMaxDevices);
+  void* a = g_scratch_addr[device].load(std::memory_order_acquire);
+  if (!a) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    a = g_scratch_addr[device].load(std::memory_order_relaxed);
+    if (!a) {
+      const hipError_t e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+      if (!a) return fail(CCV1D_ERR_HIP, "hipGetSymbolAddress(scratch) returned no address");
+      g_scratch_addr[device].store(a, std::memory_order_release);
+    }
+  }
+  *addr = a;
+  return CCV1D_OK;
+}
+
 // A validated backward request: the kernel parameters, the path, the tiling and the workspace it
 // needs, with everything but the workspace address filled in. Planning makes no HIP call, so a
 // request is refused (status and message) before anything touches a device.
@@ -609,6 +643,38 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
     return fail(CCV1D_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes,
                 pl.need);
   return run_bwd(pl, workspace, device, stream, timed);
+}
+
+int ccv1d_bwd_noalloc(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+                      const void* weight, int weight_dtype, const void* bias, int bias_dtype,
+                      const int32_t* seq_idx, const void* initial_states, int init_dtype,
+                      const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
+                      const void* dfinal_states, void* dx, void* dinitial_states, void* dweight,
+                      void* dbias, int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+                      int silu, int device, void* stream) {
+  g_last_error.clear();
+  const bool timed = take_timing_request();
+  BwdPlan pl;
+  // The scratch is 256-byte aligned, as the vectorised backward's partial rows require.
+  int rc = plan_bwd(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
+                    seq_idx, initial_states, init_dtype, dout, dout_stride_b, dout_stride_t,
+                    dfinal_states, dx, dinitial_states, dweight, dbias, true, batch, seqlen, dim,
+                    width, silu, pl);
+  if (rc) return rc;
+  if (pl.need > (size_t)CCV1D_NOALLOC_SCRATCH_BYTES)
+    return fail(CCV1D_ERR_WORKSPACE,
+                "ccv1d_bwd_noalloc: this shape needs %zu bytes of partial sums and the built-in "
+                "scratch holds %zu; call ccv1d_bwd with a workspace instead",
+                pl.need, (size_t)CCV1D_NOALLOC_SCRATCH_BYTES);
+  if (pl.skip) return CCV1D_OK;
+  void* ws = nullptr;
+  {
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "hipSetDevice");
+    rc = scratch_on_current_device(device, &ws);
+    if (rc) return rc;
+  }
+  return run_bwd(pl, ws, device, stream, timed);
 }
 
 }  // extern "C"

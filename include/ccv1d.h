@@ -128,6 +128,32 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
               int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
               int silu, int device, void* stream);
 
+/* Allocation-free backward. It has no counterpart in the reference: it is for callers that cannot
+ * allocate device memory or pass a workspace (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Arguments and results are those of ccv1d_bwd without the
+ * workspace: the fp32 partial sums of dweight/dbias go to a scratch array built into the library,
+ * CCV1D_NOALLOC_SCRATCH_BYTES bytes on every device it runs on, held until the process ends. The
+ * call allocates nothing.
+ *  - Shapes whose partial sums need more (ccv1d_bwd_workspace_bytes() gives an upper bound) are
+ *    refused with CCV1D_ERR_WORKSPACE before anything is launched.
+ *  - Calls that overlap on one device share its scratch and race: the caller orders them (one
+ *    stream, or events between streams). The scratch keeps the last call's contents; each call
+ *    writes every partial sum before reading it, so nothing needs clearing.
+ *  - The first call on a device resolves the scratch's device address (hipGetSymbolAddress); make
+ *    it outside stream capture. */
+#define CCV1D_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+int ccv1d_bwd_noalloc(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+                      const void* weight, int weight_dtype,
+                      const void* bias, int bias_dtype,
+                      const int32_t* seq_idx,
+                      const void* initial_states, int init_dtype,
+                      const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
+                      const void* dfinal_states,
+                      void* dx, void* dinitial_states, void* dweight, void* dbias,
+                      int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+                      int silu, int device, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

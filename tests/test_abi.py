@@ -26,8 +26,9 @@ def _declared():
 
 
 def test_header_declares_the_entry_points():
-    assert _declared() == ["ccv1d_abi_version", "ccv1d_bwd", "ccv1d_bwd_workspace_bytes",
-                           "ccv1d_fwd", "ccv1d_last_error", "ccv1d_time_main_kernel"]
+    assert _declared() == ["ccv1d_abi_version", "ccv1d_bwd", "ccv1d_bwd_noalloc",
+                           "ccv1d_bwd_workspace_bytes", "ccv1d_fwd", "ccv1d_last_error",
+                           "ccv1d_time_main_kernel"]
 
 
 def test_library_exports_every_declared_symbol():
@@ -110,6 +111,48 @@ def test_bwd_rejects_invalid_arguments(kw, code, msg):
     lib = _ffi.load()
     assert _bwd(lib, **kw) == code
     assert msg in lib.ccv1d_last_error().decode()
+
+
+def _bwd_noalloc(lib, **kw):
+    a = dict(x=1 << 20, xdt=2, w=1 << 21, b=None, init=None, dy=1 << 22, dfin=None, dx=1 << 23,
+             dinit=None, dw=1 << 24, db=None, B=1, T=4, D=8, W=4, seq=None)
+    a.update(kw)
+    return lib.ccv1d_bwd_noalloc(a["x"], 0, 8 if a["D"] == 8 else a["D"], a["xdt"], a["w"], 0,
+                                 a["b"], 0, a["seq"], a["init"], 0, a["dy"], 0,
+                                 8 if a["D"] == 8 else a["D"], a["dfin"], a["dx"], a["dinit"],
+                                 a["dw"], a["db"], a["B"], a["T"], a["D"], a["W"], 1, 0, None)
+
+
+def _noalloc_limit():
+    m = re.search(r"#define CCV1D_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", _header())
+    return int(m.group(1)) << int(m.group(2))
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(db=1 << 25), 1, "dbias"),
+    (dict(dinit=1 << 25), 1, "initial_states"),
+    (dict(dy=None), 1, "dout or dx"),
+    (dict(W=1), 1, "width"),
+    # partial sums beyond the built-in scratch: B * (T / 64 rows) partial rows of 5 * D floats
+    (dict(B=64, T=65536, D=4096), 3, "scratch"),
+])
+def test_bwd_noalloc_rejects_before_any_hip_call(kw, code, msg):
+    """The allocation-free backward validates and sizes the request before it touches a device
+    (here there is none): bad arguments and shapes whose partial sums exceed its scratch are
+    refused with the documented codes."""
+    lib = _ffi.load()
+    assert _bwd_noalloc(lib, **kw) == code
+    assert msg in lib.ccv1d_last_error().decode()
+
+
+def test_bwd_noalloc_limit_matches_workspace_sizing():
+    """The scratch limit of the header bounds the shapes the allocation-free backward accepts: the
+    benchmark shape fits, and the refused shape above needs more than the limit."""
+    lib = _ffi.load()
+    limit = _noalloc_limit()
+    assert limit == 32 << 20
+    assert lib.ccv1d_bwd_workspace_bytes(4, 8192, 1024, 4, 2) <= limit
+    assert lib.ccv1d_bwd_workspace_bytes(64, 65536, 4096, 4, 2) > limit
 
 
 def test_timing_request_needs_both_events_or_neither():
