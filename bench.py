@@ -81,10 +81,38 @@ def _warm(graph, min_replays, min_ms=MIN_WARMUP_MS):
     return n
 
 
+_SPIN_CYCLES_PER_MS = None
+
+
+def _spin_cycles_per_ms():
+    """Cycles of torch's bounded spin kernel (torch.cuda._sleep) per millisecond on this device,
+    measured once."""
+    global _SPIN_CYCLES_PER_MS
+    if _SPIN_CYCLES_PER_MS is None:
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1 << 16)  # first launch outside the measurement
+        s0.record()
+        torch.cuda._sleep(1 << 20)
+        s1.record()
+        torch.cuda.synchronize()
+        _SPIN_CYCLES_PER_MS = (1 << 20) / max(s0.elapsed_time(s1), 1e-3)
+    return _SPIN_CYCLES_PER_MS
+
+
+# Device time queued ahead of a timed region: a replayed graph reaches the device only after the
+# host has launched it (tens of microseconds for the first one), so a timed region that starts on an
+# idle device would count that host latency as device time, about 1.5 us per step when only 20
+# steps are timed. A bounded spin kernel keeps the device busy while the host queues the start
+# event and the replays; the start event then executes right before the first replay.
+LEAD_MS = 0.5
+
+
 def _time_graphs(seq):
-    """Device time of replaying the graphs in `seq` in order (events around the whole sequence)."""
+    """Device time of replaying the graphs in `seq` in order: events around the whole sequence,
+    queued behind LEAD_MS of spin so the device never waits for the host inside the region."""
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(_spin_cycles_per_ms() * LEAD_MS))
     start.record()
     for g in seq:
         g.replay()
@@ -127,13 +155,7 @@ def passes_in_step(sets, w, b, steps):
             ev[2].record()
         return r
 
-    # spin-kernel cycles per millisecond on this device
-    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s0.record()
-    torch.cuda._sleep(1 << 20)
-    s1.record()
-    torch.cuda.synchronize()
-    cycles_per_ms = (1 << 20) / max(s0.elapsed_time(s1), 1e-3)
+    cycles_per_ms = _spin_cycles_per_ms()
     # host time to enqueue one step, measured on the warm-up steps
     k, t0 = 0, time.perf_counter()
     while k < 2 * n or (time.perf_counter() - t0) * 1e3 < MIN_WARMUP_MS:

@@ -329,6 +329,26 @@ __device__ __forceinline__ float dsilu_times(float dy, float z) {
   return dy * s * fmaf(z, 1.0f - s, 1.0f);
 }
 
+// The vectorised backward evaluates silu' in the base-2 domain. Its weights and bias are
+// pre-multiplied by -log2(e), so the tap chain yields y = -log2(e) * z, the argument of exp2
+// itself, and no per-element multiply forms it. With e = 2^y = exp(-z) and s = 1 / (1 + e):
+//   silu'(z) = s * (1 + z * (1 - s)),  z = -ln2 * y
+//   -ln2 * silu'(z) = s * fma(y, ln2^2 * (1 - s), -ln2)
+// so g~ = dy * s * fma(y, fma(s, -ln2^2, ln2^2), -ln2) = -ln2 * g costs the same four operations
+// as g. dx = sum_j (-log2(e) w) * (-ln2 g) = sum_j w * g needs no correction (log2(e) * ln2 = 1);
+// the dweight/dbias sums, accumulated from g~, are multiplied by -log2(e) once per tile.
+constexpr float kNegLog2e = -1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLn2Sq = 0.4804530139182014f;
+
+// g~ = -ln2 * dy * silu'(z) from y = -log2(e) * z (see above). Non-finite inputs propagate as in
+// the unscaled form: z = +-inf gives 0 * inf = NaN where the reference's expression does.
+__device__ __forceinline__ float dsilu_scaled(float dy, float y) {
+  const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y));
+  const float u = fmaf(y, fmaf(s, -kLn2Sq, kLn2Sq), -kLn2);
+  return (dy * s) * u;
+}
+
 // Rows whose sequence ids a wave of the vectorised kernels reads up front (RowIds): its tile and both
 // halos must fit.
 constexpr int kRowIds = 128;

@@ -36,18 +36,21 @@ __device__ __forceinline__ void load_taps(const void* w, int w_dt, const void* b
   }
 }
 
-// Pre-activation of one row (causal_conv1d.py:129-138), in the reference's order:
+// Pre-activation of one row (causal_conv1d.py:129-138). In the reference's order:
 //   z = w[P] * x[t]; z = fma(w[k], x[t-P+k], z) for k = 0..P-1 (masked by sequence equality);
 //   z += bias (-0.0 without one); with ZERO_PAD, z = 0 on padding rows (sequence id < 0).
+// With BIAS_FIRST the bias enters the first term instead, z = fma(w[P], x[t], bias), which saves
+// the final add (a different rounding order: used where silu follows, whose results are held to
+// tolerance; without an activation the forward keeps the reference's order bit for bit).
 // xw holds rows t-P .. t-1, sw their sequence ids; xc is row t and st its sequence id.
-template <int W, int CPL, bool SEQ, bool ZERO_PAD>
+template <int W, int CPL, bool SEQ, bool ZERO_PAD, bool BIAS_FIRST = false>
 __device__ __forceinline__ void conv_row(const float (&wv)[W][CPL], const float (&bv)[CPL],
                                          const float (&xw)[W - 1][CPL],
                                          const int32_t (&sw)[W - 1], const float (&xc)[CPL],
                                          int32_t st, float (&z)[CPL]) {
   constexpr int P = W - 1;
 #pragma unroll
-  for (int i = 0; i < CPL; ++i) z[i] = wv[P][i] * xc[i];
+  for (int i = 0; i < CPL; ++i) z[i] = BIAS_FIRST ? fmaf(wv[P][i], xc[i], bv[i]) : wv[P][i] * xc[i];
 #pragma unroll
   for (int k = 0; k < P; ++k) {
     const bool m = !SEQ || sw[k] == st;
@@ -57,8 +60,10 @@ __device__ __forceinline__ void conv_row(const float (&wv)[W][CPL], const float 
       z[i] = m ? f : z[i];
     }
   }
+  if (!BIAS_FIRST) {
 #pragma unroll
-  for (int i = 0; i < CPL; ++i) z[i] += bv[i];
+    for (int i = 0; i < CPL; ++i) z[i] += bv[i];
+  }
   if (SEQ && ZERO_PAD && st < 0) {
 #pragma unroll
     for (int i = 0; i < CPL; ++i) z[i] = 0.0f;
@@ -174,7 +179,7 @@ struct FwdLane {
   __device__ __forceinline__ raw row(const raw xr, int32_t st) {
     float xc[CPL], z[CPL];
     IO::unpack(xr, xc);
-    conv_row<W, CPL, SEQ, true>(wv, bv, xw, sw, xc, st, z);
+    conv_row<W, CPL, SEQ, true, SILU>(wv, bv, xw, sw, xc, st, z);
     if (SILU) {
 #pragma unroll
       for (int i = 0; i < CPL; ++i) z[i] = z[i] * sigmoid_f(z[i]);
@@ -199,7 +204,7 @@ struct FwdLaneRev {
   // Output row t, then the window moves down one row: `xr` (row t-P-1, sequence id `st`) enters.
   __device__ __forceinline__ raw row(const raw xr, int32_t st) {
     float z[CPL];
-    conv_row<W, CPL, SEQ, true>(wv, bv, reinterpret_cast<const float(&)[P][CPL]>(xv),
+    conv_row<W, CPL, SEQ, true, SILU>(wv, bv, reinterpret_cast<const float(&)[P][CPL]>(xv),
                                 reinterpret_cast<const int32_t(&)[P]>(sv), xv[P], sv[P], z);
     if (SILU) {
 #pragma unroll
@@ -479,10 +484,12 @@ struct BwdLane {
       IO::unpack(yr, g);
     }
     if (SILU && !PAD) {
-      float z[CPL];
-      conv_row<W, CPL, SEQ, false>(wv, bv, xw, sw, xc, st, z);
+      // wv and bv hold -log2(e) times the weights and bias: y = -log2(e) * z, and g is the
+      // scaled gradient -ln2 * dout * silu'(z) (dsilu_scaled).
+      float y[CPL];
+      conv_row<W, CPL, SEQ, false, true>(wv, bv, xw, sw, xc, st, y);
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) g[i] = dsilu_times(g[i], z[i]);
+      for (int i = 0; i < CPL; ++i) g[i] = dsilu_scaled(g[i], y[i]);
     }
     if (SEQ && st < 0) {
 #pragma unroll
@@ -625,6 +632,15 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
     }
     load(Ax, Ay, t_main);
     load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
+    if (SILU && !PAD) {
+      // silu' in the base-2 domain (dsilu_scaled): weights and bias times -log2(e).
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+#pragma unroll
+        for (int k = 0; k < W; ++k) s.wv[k][i] *= kNegLog2e;
+        s.bv[i] *= kNegLog2e;
+      }
+    }
     // Every tile is at least min_tile_rows(W) > P rows long (the host's tiling; static_assert in
     // ccv1d_api.hip), so a tile starts at row 0 or at a row >= P: a window not in x is the first
     // tile's, the P initial-state rows (or zeros).
@@ -719,6 +735,16 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
         shift_in(s.gw, zero);
         if (SEQ) shift_in(s.sw, -1);
       }
+    }
+  }
+
+  if (SILU && !PAD) {
+    // The sums were accumulated from g~ = -ln2 * g (dsilu_scaled).
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+#pragma unroll
+      for (int k = 0; k < W; ++k) s.dw[k][i] *= kNegLog2e;
+      s.db[i] *= kNegLog2e;
     }
   }
 
