@@ -232,6 +232,16 @@ Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
   return bwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);
 }
 
+// Workspace of the backward: the fp32 partial rows of dweight/dbias, (rows, W + 1, D) floats, and
+// for widths above kMaxGenericW after them, 256-byte aligned, the fp32 g buffer (B, T, D).
+size_t partial_bytes(int64_t rows, int64_t W, int64_t D) {
+  return (size_t)(rows * (W + 1) * D * (int64_t)sizeof(float));
+}
+size_t g_buffer_bytes(int64_t B, int64_t T, int64_t D) {
+  return (size_t)(B * T * D * (int64_t)sizeof(float));
+}
+size_t g_buffer_offset(size_t partials) { return (partials + 255) & ~(size_t)255; }
+
 Tiling generic_tiling(int64_t T) {
   Tiling t{};
   t.L = kGenericL;
@@ -356,7 +366,6 @@ int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
     if (fast) {
       tl = fwd_fast_tiling(B, T, D, W, x_dtype);
     } else {
-      if (W > kMaxGenericW) return fail(CCV1D_ERR_UNSUPPORTED, "width > %d", kMaxGenericW);
       tl = generic_tiling(T);
       if (B * tl.nT >= (int64_t(1) << 31) || cdiv(D, 64) > 65535)
         return fail(CCV1D_ERR_UNSUPPORTED, "shape too large for the generic kernel");
@@ -433,7 +442,9 @@ size_t ccv1d_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t dim, int
     const int64_t fr = B * bwd_fast_tiling(B, T, D, W, x_dtype).nTB;
     if (fr > rows) rows = fr;
   }
-  return (size_t)(rows * (W + 1) * D * (int64_t)sizeof(float));
+  size_t n = partial_bytes(rows, W, D);
+  if (W > kMaxGenericW) n = g_buffer_offset(n) + g_buffer_bytes(B, T, D);
+  return n;
 }
 
 }  // extern "C"
@@ -481,7 +492,9 @@ struct BwdPlan {
   bool skip = false;   // dim == 0: nothing to do
   bool empty = false;  // batch == 0 or seqlen == 0: the fill path
   bool fast = false;
+  bool wide = false;   // generic path above kMaxGenericW: g goes through the workspace
   int x_dt = 0;
+  size_t g_off = 0;    // byte offset of the g buffer in the workspace (wide)
   size_t need = 0;     // workspace bytes the launches use
 };
 
@@ -562,14 +575,18 @@ int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
     p.y_bytes = slab_bytes(x_dtype, T, D, dout_stride_t);
     p.o_bytes = slab_bytes(x_dtype, T, D, D);
   } else {
-    if (W > kMaxGenericW) return fail(CCV1D_ERR_UNSUPPORTED, "width > %d", kMaxGenericW);
     p.tl = generic_tiling(T);
     rows = B * p.tl.nT;
     if (rows >= (int64_t(1) << 31) || cdiv(D, 64) > 65535)
       return fail(CCV1D_ERR_UNSUPPORTED, "shape too large for the generic kernel");
+    pl.wide = W > kMaxGenericW;
   }
   r.Pn = (int32_t)rows;
-  pl.need = (size_t)(rows * (W + 1) * D * (int64_t)sizeof(float));
+  pl.need = partial_bytes(rows, W, D);
+  if (pl.wide) {
+    pl.g_off = g_buffer_offset(pl.need);
+    pl.need = pl.g_off + g_buffer_bytes(B, T, D);
+  }
   return CCV1D_OK;
 }
 
@@ -604,6 +621,14 @@ int run_bwd(BwdPlan& pl, void* workspace, int device, void* stream, bool timed) 
         case CCV1D_BF16: e = launch_bwd_fast_t<__bf16>(p, s); break;
         case CCV1D_F16: e = launch_bwd_fast_t<_Float16>(p, s); break;
         default: e = launch_bwd_fast_t<float>(p, s); break;
+      }
+    } else if (pl.wide) {
+      float* G = reinterpret_cast<float*>(static_cast<char*>(workspace) + pl.g_off);
+      switch (pl.x_dt) {
+        case CCV1D_BF16: e = launch_bwd_wide_t<__bf16>(p, G, s); break;
+        case CCV1D_F16: e = launch_bwd_wide_t<_Float16>(p, G, s); break;
+        case CCV1D_F32: e = launch_bwd_wide_t<float>(p, G, s); break;
+        default: e = launch_bwd_wide_t<double>(p, G, s); break;
       }
     } else {
       switch (pl.x_dt) {

@@ -173,6 +173,125 @@ __global__ __launch_bounds__(64) void bwd_generic_kernel(const BwdParams p) {
   if (p.has_bias) pp[(int64_t)W * D] = db;
 }
 
+// Backward for widths whose g ring would not fit LDS (above kMaxGenericW): the gradient g of the
+// pre-activation goes to a fp32 buffer G (batch, seqlen, dim) in the workspace, and a second kernel
+// forms dx and the dweight/dbias partial rows from it, so no on-chip storage grows with the width.
+// Same row semantics, summation orders and partial-row layout as bwd_generic_kernel.
+
+// G[b, t, c] = dout * silu'(z) (or dout), 0 on padding rows (causal_conv1d.py:274-288).
+template <typename TX>
+__global__ __launch_bounds__(64) void bwd_g_kernel(const BwdParams p, float* G) {
+  const int c = blockIdx.y * 64 + threadIdx.x;
+  if (c >= p.D) return;
+  const int tile = blockIdx.x % p.tl.nT;
+  const int b = blockIdx.x / p.tl.nT;
+  const int T = p.T, D = p.D, W = p.W, P = W - 1;
+  const bool has_init = p.has_init;
+  GenRow<TX> xx;
+  xx.xb = static_cast<const TX*>(p.x) + (int64_t)b * p.s_xb + c;
+  xx.s_xt = p.s_xt;
+  xx.initb = has_init
+                 ? static_cast<const char*>(p.init) + ((int64_t)b * P * D + c) * dt_size(p.i_dt)
+                 : nullptr;
+  xx.i_dt = p.i_dt;
+  xx.P = P;
+  xx.D = D;
+  const TX* yb = static_cast<const TX*>(p.dy) + (int64_t)b * p.s_yb + c;
+  const int32_t* sb = p.seq ? p.seq + (int64_t)b * T : nullptr;
+  const float bias = p.has_bias ? ld_any(p.bias, c, p.b_dt) : 0.0f;
+  float* gb = G + (int64_t)b * T * D + c;
+  const int t0 = tile * p.tl.L;
+  const int t1 = min(t0 + p.tl.L, T);
+  for (int t = t0; t < t1; ++t) {
+    const int32_t st = sb ? sb[t] : 0;
+    float g = static_cast<float>(yb[(int64_t)t * p.s_yt]);
+    if (p.silu) {
+      float z = gen_conv(xx, p.w, p.w_dt, c, W, sb, T, has_init, t, st);
+      if (p.has_bias) z += bias;
+      g = dsilu_times(g, z);
+    }
+    if (sb && st < 0) g = 0.0f;
+    gb[(int64_t)t * D] = g;
+  }
+}
+
+// dx (and the initial-state gradient) of the tile's rows from G, and the tile's dweight/dbias
+// partial row (row b * nT + tile of `part`). dweight is accumulated KB taps at a time: each block
+// walks the tile's rows once, so g is read W / KB times per row instead of W times.
+template <typename TX, int KB = 8>
+__global__ __launch_bounds__(64) void bwd_wide_kernel(const BwdParams p, const float* G) {
+  const int c = blockIdx.y * 64 + threadIdx.x;
+  if (c >= p.D) return;
+  const int tile = blockIdx.x % p.tl.nT;
+  const int b = blockIdx.x / p.tl.nT;
+  const int T = p.T, D = p.D, W = p.W, P = W - 1;
+  const bool has_init = p.has_init;
+  GenRow<TX> xx;
+  xx.xb = static_cast<const TX*>(p.x) + (int64_t)b * p.s_xb + c;
+  xx.s_xt = p.s_xt;
+  const int isz = dt_size(p.i_dt);
+  xx.initb = has_init ? static_cast<const char*>(p.init) + ((int64_t)b * P * D + c) * isz : nullptr;
+  xx.i_dt = p.i_dt;
+  xx.P = P;
+  xx.D = D;
+  TX* dxb = static_cast<TX*>(p.dx) + (int64_t)b * T * D + c;
+  void* dinitb =
+      p.need_dinit ? static_cast<char*>(p.dinit) + ((int64_t)b * P * D + c) * isz : nullptr;
+  const TX* dfb = p.has_dfinal ? static_cast<const TX*>(p.dfin) + (int64_t)b * P * D + c : nullptr;
+  const int32_t* sb = p.seq ? p.seq + (int64_t)b * T : nullptr;
+  const float* gb = G + (int64_t)b * T * D + c;
+  const int64_t wo = (int64_t)c * W;
+  // g of row `row` of concat(initial_states, x): 0 outside [0, T).
+  auto g_at = [&](int row) { return (row >= 0 && row < T) ? gb[(int64_t)row * D] : 0.0f; };
+
+  const int t0 = tile * p.tl.L;
+  const int own_end = min(t0 + p.tl.L, T);
+  const int emit_lo = (tile == 0 && p.need_dinit) ? -P : t0;
+  // dx[row] = w[P] g[row] + sum_{j=1..P} m_j w[P-j] g[row+j] (+ dfinal), causal_conv1d.py:290-311.
+  for (int row = emit_lo; row < own_end; ++row) {
+    const int32_t s0 = sb ? seq_at(sb, row, T, has_init) : 0;
+    float dx = ld_any(p.w, wo + P, p.w_dt) * g_at(row);
+    for (int j = 1; j <= P; ++j) {
+      if (sb && seq_at(sb, row + j, T, has_init) != s0) continue;
+      dx = fmaf(ld_any(p.w, wo + P - j, p.w_dt), g_at(row + j), dx);
+    }
+    if (dfb) {
+      const int f = row - (T - P);
+      if (f >= 0 && f < P) dx += static_cast<float>(dfb[(int64_t)f * D]);
+    }
+    if (row >= 0) dxb[(int64_t)row * D] = static_cast<TX>(dx);
+    else st_any(dinitb, (int64_t)(row + P) * D, p.i_dt, dx);
+  }
+
+  // dweight[c, k] over the tile's own rows, ascending t for every k (causal_conv1d.py:313-321).
+  float* pp = p.part + ((int64_t)b * p.tl.nT + tile) * (W + 1) * D + c;
+  for (int kb = 0; kb < W; kb += KB) {
+    float acc[KB];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) acc[j] = 0.0f;
+    for (int t = t0; t < own_end; ++t) {
+      const float g = gb[(int64_t)t * D];
+      const int32_t st = sb ? sb[t] : 0;
+#pragma unroll
+      for (int j = 0; j < KB; ++j) {
+        const int k = kb + j;
+        if (k >= W) break;
+        const int r = t - P + k;
+        if (k < P && sb && seq_at(sb, r, T, has_init) != st) continue;
+        acc[j] = fmaf(g, xx(r), acc[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      if (kb + j < W) pp[(int64_t)(kb + j) * D] = acc[j];
+  }
+  if (p.has_bias) {
+    float db = 0.0f;
+    for (int t = t0; t < own_end; ++t) db += gb[(int64_t)t * D];
+    pp[(int64_t)W * D] = db;
+  }
+}
+
 // dweight[d, k] = sum_p part[p, k, d] and dbias[d] = sum_p part[p, W, d] (causal_conv1d.py:344-374),
 // in an order fixed by Pn alone: wave w of NWR adds rows w, w + NWR, ... in ascending order, then the
 // NWR wave sums are added in wave order.

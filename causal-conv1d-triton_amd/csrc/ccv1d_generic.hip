@@ -18,6 +18,18 @@ hipError_t launch_bwd_generic_t(const BwdParams& p, hipStream_t s) {
   return launch(reinterpret_cast<const void*>(&bwd_generic_kernel<TX>), grid, dim3(64), shmem, s, &p);
 }
 
+template <typename TX>
+hipError_t launch_bwd_wide_t(const BwdParams& p, float* G, hipStream_t s) {
+  const dim3 grid((unsigned)((int64_t)p.B * p.tl.nT), (unsigned)((p.D + 63) / 64));
+  BwdParams pc = p;
+  void* args[] = {&pc, &G};
+  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&bwd_g_kernel<TX>), grid, dim3(64),
+                                 args, 0, s);
+  if (e != hipSuccess) return e;
+  return launch_args(reinterpret_cast<const void*>(&bwd_wide_kernel<TX>), grid, dim3(64), 0, s,
+                     args);
+}
+
 template hipError_t launch_fwd_generic_t<float>(const FwdParams&, hipStream_t);
 template hipError_t launch_fwd_generic_t<_Float16>(const FwdParams&, hipStream_t);
 template hipError_t launch_fwd_generic_t<__bf16>(const FwdParams&, hipStream_t);
@@ -26,6 +38,10 @@ template hipError_t launch_bwd_generic_t<float>(const BwdParams&, hipStream_t);
 template hipError_t launch_bwd_generic_t<_Float16>(const BwdParams&, hipStream_t);
 template hipError_t launch_bwd_generic_t<__bf16>(const BwdParams&, hipStream_t);
 template hipError_t launch_bwd_generic_t<double>(const BwdParams&, hipStream_t);
+template hipError_t launch_bwd_wide_t<float>(const BwdParams&, float*, hipStream_t);
+template hipError_t launch_bwd_wide_t<_Float16>(const BwdParams&, float*, hipStream_t);
+template hipError_t launch_bwd_wide_t<__bf16>(const BwdParams&, float*, hipStream_t);
+template hipError_t launch_bwd_wide_t<double>(const BwdParams&, float*, hipStream_t);
 
 hipError_t launch_reduce(const ReduceParams& p, hipStream_t s) {
   const int64_t n = (int64_t)(p.W + (p.has_bias ? 1 : 0)) * p.D;

@@ -45,7 +45,8 @@ template <typename TX> struct BwdCfg {
 constexpr int kMaxFastW = 16;    // widths 2..kMaxFastW have register-window kernels
 constexpr int kFwdWideW = 9;     // first width whose forward always uses FwdCfg::CPL_SMALL
 constexpr int kBwdWideW = 6;     // first width whose backward uses BwdCfg::CPL_WIDE
-constexpr int kMaxGenericW = 128;  // LDS ring of the generic backward: 2 * W * 64 * 4 bytes
+constexpr int kMaxGenericW = 128;  // LDS ring of the generic backward: 2 * W * 64 * 4 bytes; wider
+                                   // backwards keep g in the workspace (bwd_g/bwd_wide kernels)
 constexpr int kReduceNW = 16;    // waves per reduction workgroup
 constexpr int kGenericL = 64;    // rows per tile of the generic kernels
 
@@ -61,9 +62,8 @@ inline KernelEvents& kernel_events() {
   return e;
 }
 
-inline hipError_t launch(const void* kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t s,
-                         const void* params) {
-  void* args[] = {const_cast<void*>(params)};
+inline hipError_t launch_args(const void* kernel, dim3 grid, dim3 block, size_t shmem,
+                              hipStream_t s, void** args) {
   KernelEvents& ev = kernel_events();
   if (ev.armed) {
     // HIP sets both events from the dispatch's own start and end timestamps.
@@ -71,6 +71,12 @@ inline hipError_t launch(const void* kernel, dim3 grid, dim3 block, size_t shmem
     return hipExtLaunchKernel(kernel, grid, block, args, shmem, s, ev.start, ev.stop, 0);
   }
   return hipLaunchKernel(kernel, grid, block, args, shmem, s);
+}
+
+inline hipError_t launch(const void* kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t s,
+                         const void* params) {
+  void* args[] = {const_cast<void*>(params)};
+  return launch_args(kernel, grid, block, shmem, s, args);
 }
 
 // The vectorised kernels of widths below kFwdWideW and of widths kFwdWideW..kMaxFastW are
@@ -96,6 +102,10 @@ template <typename TX>
 hipError_t launch_fwd_generic_t(const FwdParams& p, hipStream_t s);
 template <typename TX>
 hipError_t launch_bwd_generic_t(const BwdParams& p, hipStream_t s);
+// Backward above kMaxGenericW: g to the fp32 buffer G of (batch, seqlen, dim) floats, then dx and
+// the partial rows from it (the second is the main kernel for ccv1d_time_main_kernel).
+template <typename TX>
+hipError_t launch_bwd_wide_t(const BwdParams& p, float* G, hipStream_t s);
 hipError_t launch_reduce(const ReduceParams& p, hipStream_t s);
 hipError_t launch_fill(void* dst, int dst_dt, const void* src, int src_dt, int64_t n, hipStream_t s);
 

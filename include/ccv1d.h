@@ -47,7 +47,9 @@ enum ccv1d_dtype { CCV1D_F32 = 0, CCV1D_F16 = 1, CCV1D_BF16 = 2, CCV1D_F64 = 3 }
 enum ccv1d_status {
   CCV1D_OK = 0,
   CCV1D_ERR_INVALID = 1,     /* bad argument: null pointer, negative size, width < 2, bad dtype code */
-  CCV1D_ERR_UNSUPPORTED = 2, /* valid request outside what the kernels implement (e.g. width > 128) */
+  CCV1D_ERR_UNSUPPORTED = 2, /* valid request outside what the kernels implement (a grid beyond the
+                                generic kernels' limits: batch * ceil(seqlen / 64) >= 2^31, or more
+                                than 65535 * 64 channels on rows that need them) */
   CCV1D_ERR_WORKSPACE = 3,   /* workspace missing or smaller than ccv1d_bwd_workspace_bytes() */
   CCV1D_ERR_HIP = 4          /* a HIP runtime call or kernel launch failed */
 };
@@ -94,8 +96,10 @@ int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
               int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
               int silu, int device, void* stream);
 
-/* Bytes of device workspace ccv1d_bwd needs for this shape (fp32 partial sums of dweight/dbias; the
- * reference allocates the same kind of buffer at causal_conv1d.py:493). 0 for empty shapes. */
+/* Bytes of device workspace ccv1d_bwd needs for this shape: fp32 partial sums of dweight/dbias (the
+ * reference allocates the same kind of buffer at causal_conv1d.py:493) and, for widths above 128,
+ * an fp32 buffer of batch * seqlen * dim values for the gradient of the pre-activation. An upper
+ * bound over every path the shape can take; 0 for empty shapes. */
 size_t ccv1d_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
                                  int x_dtype);
 

@@ -55,6 +55,16 @@ def test_workspace_bytes():
     assert n % (5 * 1024 * 4) == 0
 
 
+def test_workspace_bytes_of_wide_widths():
+    """Above width 128 the backward's workspace holds the partial rows (one per 64-row tile, W + 1
+    rows of dim floats) and, 256-byte aligned after them, one fp32 g value per element."""
+    lib = _ffi.load()
+    for B, T, D, W in ((2, 300, 100, 129), (4, 8192, 1024, 200), (1, 1, 8, 257)):
+        part = B * -(-T // 64) * (W + 1) * D * 4
+        want = (part + 255) // 256 * 256 + B * T * D * 4
+        assert lib.ccv1d_bwd_workspace_bytes(B, T, D, W, 2) == want
+
+
 def _fwd(lib, **kw):
     a = dict(x=1 << 20, sxb=0, sxt=8, xdt=2, w=1 << 21, wdt=0, b=None, bdt=0, seq=None, init=None,
              idt=0, out=1 << 22, fin=None, B=1, T=4, D=8, W=4, silu=1, dev=0, stream=None)
@@ -104,7 +114,8 @@ def _bwd(lib, **kw):
     (dict(seq=1 << 25, dfin=1 << 26), 1, "seq_idx"),
     (dict(ws=None, wsb=0), 3, "workspace"),
     (dict(ws=1 << 27, wsb=16), 3, "workspace"),
-    (dict(W=200, ws=1 << 27, wsb=1 << 30), 2, "width"),
+    # widths above 128 also keep g in the workspace: one partial row is not enough
+    (dict(W=200, ws=1 << 27, wsb=201 * 8 * 4), 3, "workspace"),
 ])
 def test_bwd_rejects_invalid_arguments(kw, code, msg):
     # every case fails validation, so no HIP call is reached
@@ -207,7 +218,7 @@ def test_native_fwd_rejects_invalid_arguments(kw, msg):
 @pytest.mark.parametrize("kw,code,msg", [
     (dict(db=1 << 25), 1, "dbias"),
     (dict(ws=None, wsb=0), 3, "workspace"),
-    (dict(W=200, ws=1 << 27, wsb=1 << 30), 2, "width"),
+    (dict(W=200, ws=1 << 27, wsb=201 * 8 * 4), 3, "workspace"),
 ])
 def test_native_bwd_rejects_invalid_arguments(kw, code, msg):
     lib = _ffi.load()

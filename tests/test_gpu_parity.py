@@ -533,13 +533,33 @@ def test_empty_inputs(shape):
         assert torch.equal(init.grad, dfin.to(init.dtype))
 
 
-def test_width_limit_error():
-    from causal_conv1d_triton._ffi import CCV1DError
+@pytest.mark.parametrize("W", [129, 200, 257])
+@pytest.mark.parametrize("D", [8, 100])
+def test_widths_above_128(W, D):
+    """Any width >= 2 (reference README.md:40): above 128 the forward runs the generic kernel and
+    the backward keeps g in the workspace (bwd_g_kernel, bwd_wide_kernel). Against the oracle at
+    lengths around the window, with initial and final states and their gradients."""
+    for T in (1, W - 1, W + 1, 300):
+        init = T % 2 == 1
+        inp = make_inputs(7 * W + T + D, 2, T, D, W, init=init)
+        gpu = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=init)
+        ref = oracle_ref(inp, True, final=True, dfinal=True, need_dinit=init)
+        compare(gpu, ref, True)
 
-    x = torch.randn(1, 8, 16, device=DEV)
-    w = torch.randn(16, 200, device=DEV)
-    with pytest.raises(CCV1DError, match="width"):
-        causal_conv1d_fn(x, w)
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("act", [None, "silu"])
+def test_width_200_seq_idx(xdt, act):
+    """Width 200 with packed sequences (padding runs, a repeated id) and initial states, in fp32
+    and fp16, with and without the activation."""
+    B, T, D, W = 2, 700, 64, 200
+    seq = varlen_seq(200, B, T, lo=40, hi=300, pad_frac=0.1)
+    seq[1, 50:90] = -3
+    inp = make_inputs(201, B, T, D, W, xdt=xdt, init=True, seq=seq, bias=act is not None)
+    gpu = run_gpu(inp, act, init_grad=True)
+    compare(gpu, oracle_ref(inp, act is not None, need_dinit=True), act is not None)
+    pad = seq < 0
+    assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0)
 
 
 # ------------------------------------------------------------------------------------------------

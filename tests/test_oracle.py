@@ -107,3 +107,27 @@ def test_torch_cpu_baseline_matches_oracle(silu, bias):
     np.testing.assert_allclose(grads[1][:, 0, :].numpy(), dw, rtol=1e-5, atol=1e-4)
     if bias:
         np.testing.assert_allclose(grads[2].numpy(), db, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("W", [129, 200, 257])
+def test_wide_widths_vs_closed_form(W):
+    """Widths above 128 (the reference allows any width >= 2, README.md:40): the oracle against the
+    float64 grouped F.conv1d closed form and its autograd, at lengths around the window."""
+    for T in (1, W - 1, W + 1, 300):
+        c = pins.make_case(seed=W + T, B=2, T=T, D=3, W=W, init=True, dfinal=True, silu=True)
+        ok, det = pins.check_fwd_closed_form(c)
+        assert ok, f"T={T}: {det}"
+        ok, det = pins.check_bwd_autograd(c)
+        assert ok, f"T={T}: {det}"
+
+
+@pytest.mark.parametrize("init", [False, True])
+def test_wide_width_seq_vs_shifted_form(init):
+    """seq_idx at width 200 against the shifted-sum form with sequence masks."""
+    W = 200
+    for T in (W - 1, 450):
+        c = pins.make_case(seed=T, B=2, T=T, D=3, W=W, init=init, seq="padded", silu=True)
+        ok, det = pins.check_fwd_shifted(c)
+        assert ok, f"T={T}: {det}"
+        ok, det = pins.check_bwd_autograd(c)
+        assert ok, f"T={T}: {det}"

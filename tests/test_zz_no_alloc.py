@@ -80,6 +80,7 @@ def _seq(B, T, seed):
 CASES = [
     ("benchmark shape", dict(B=4, T=8192, D=1024, W=4, init=True)),
     ("smaller, fast kernels", dict(B=2, T=700, D=256, W=4, init=True)),
+    ("width 200: g in the scratch", dict(B=2, T=300, D=100, W=200, init=True)),
     ("generic kernels (width 20)", dict(B=2, T=333, D=100, W=20, init=True)),
     ("seq_idx, width 7", dict(B=2, T=1500, D=512, W=7, seq=True)),
     ("fp32 x, no bias", dict(B=1, T=64, D=64, W=3, xdt=torch.float32, bias=False)),
