@@ -35,6 +35,15 @@ class CCV1DError(RuntimeError):
     """A libccv1d call returned an error status."""
 
 
+# The inference forward over torch tensors in one native call (csrc/ccv1d_torch.cpp), when built.
+try:
+    from . import _ccv1d_torch as _torch_native
+except ImportError:  # not built: causal_conv1d_fn makes the call from Python
+    _torch_native = None
+else:
+    _torch_native.set_error_type(CCV1DError)
+
+
 def library_path() -> str:
     return _LIB_PATH
 

@@ -266,6 +266,17 @@ def causal_conv1d_fn(
         assert not return_final_states, "cannot return final states if seq_idx is not None"
     if final_states_out is not None:
         assert return_final_states, "final_states_out requires return_final_states=True"
+    compiling = torch.compiler.is_compiling()
+    if _ffi._torch_native is not None and not compiling:
+        # Inference on plain tensors: checks, canonicalisation, allocation and the launch in one
+        # native call (decode steps are host-bound). None: autograd must record the call, or an
+        # argument is a tensor subclass; both continue below.
+        res = _ffi._torch_native.fwd(x, weight, bias, seq_idx, initial_states,
+                                     return_final_states, silu)
+        if res is not None:
+            if final_states_out is None:
+                return res
+            return res[0], final_states_out.copy_(res[1])
     _check_inputs(x, weight, bias, seq_idx, initial_states)
     x = _channels_contiguous(x)
     weight = weight.contiguous()
@@ -277,7 +288,7 @@ def causal_conv1d_fn(
         initial_states = initial_states.contiguous()
 
     final_states = None
-    if torch.compiler.is_compiling():
+    if compiling:
         # Traced by torch.compile: the registered operators carry the passes and their autograd.
         out, final_states = _fwd_op(x, weight, bias, seq_idx, initial_states,
                                     return_final_states, silu)

@@ -405,6 +405,52 @@ def test_both_bindings_give_identical_results():
             assert torch.equal(a[k], b[k]), k
 
 
+@pytest.mark.parametrize("case", ["plain", "states", "seq_int64", "strided", "final_out",
+                                  "generic", "empty"])
+def test_native_inference_forward_matches_python_path(case):
+    """Inference calls (no autograd) go through one native call (_ccv1d_torch: checks,
+    canonicalisation, allocation, launch). The same call made from Python (the ctypes binding
+    of the same C ABI) gives identical results, bit for bit."""
+    from causal_conv1d_triton import _ffi
+    from causal_conv1d_triton.causal_conv1d import _fwd
+
+    assert _ffi._torch_native is not None
+    B, T, D, W = 3, 257, 256, 4
+    if case == "generic":
+        W = 20
+    if case == "empty":
+        T = 0
+    inp = make_inputs(90, B, T, D, W, init=case in ("states", "final_out", "empty"),
+                      seq=varlen_seq(9, B, T, lo=20, hi=90) if case == "seq_int64" else None)
+    x = inp["x"].to(DEV)
+    if case == "strided":
+        big = torch.zeros(B, T, D + 64, dtype=x.dtype, device=DEV)
+        big[..., 32:32 + D] = x
+        x = big[..., 32:32 + D]
+    w, b = inp["w"].to(DEV), inp["b"].to(DEV)
+    init = None if inp["init"] is None else inp["init"].to(DEV)
+    seq = None if inp["seq"] is None else inp["seq"].to(DEV).long()
+    final = seq is None
+    buf = torch.empty(B, W - 1, D, dtype=x.dtype, device=DEV) if case == "final_out" else None
+    with torch.no_grad():
+        got = causal_conv1d_fn(x, w, b, seq_idx=seq, initial_states=init,
+                               return_final_states=final, final_states_out=buf,
+                               activation="silu")
+        fin = torch.empty(B, W - 1, D, dtype=x.dtype, device=DEV) if final else None
+        native, _ffi._native = _ffi._native, None
+        try:
+            want = _fwd(x, w, b, None if seq is None else seq.int(), init, fin, True)
+        finally:
+            _ffi._native = native
+    torch.cuda.synchronize()
+    if final:
+        assert torch.equal(got[0], want) and torch.equal(got[1], fin)
+        if buf is not None:
+            assert got[1] is buf
+    else:
+        assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("W,xdt", [(4, torch.bfloat16), (12, torch.bfloat16), (4, torch.float64)])
 def test_kernel_timing_events(W, xdt):
     """ccv1d_time_main_kernel (fast and generic kernels): the timed launch gives bit-identical
