@@ -298,22 +298,28 @@ def _alg_bytes_general(B, T, D, W, bias, init=False, seq=False, final=False, ex=
     return fwd, bwd
 
 
-def run_configs(dev, widths=False):
+def run_configs(dev, widths=False, only=None):
     """One JSON line per BASELINE configuration 2-5 (the reference's README sweep, the Mamba-2 xBC
     shape, chunked streaming and decode with state handoff, packed varlen seq_idx): device time per
     call from replayed graphs after the usual warm-up, plus, for the latency-bound streaming and
     decode calls, the host-inclusive eager time per call. With `widths`, instead: the benchmark
     shape (bf16, bias + silu) at every width the vectorised kernels cover, forward alone and
-    forward + backward (widths 2-8, 9, 12 and 16)."""
+    forward + backward (widths 2-8, 9, 12 and 16).
+
+    `only` (a set of strings, e.g. {"2:512", "5:7"} or, with `widths`, {"8"}) restricts the run to
+    the named configurations (N, or N:T for configuration 2's lengths, N:W for configuration 5's
+    widths) or widths, so that a profiler run covers one workload."""
+    def want(cfg, sub=None):
+        return not only or str(cfg) in only or (sub is not None and f"{cfg}:{sub}" in only)
+
     from causal_conv1d_triton import causal_conv1d_fn
-    from causal_conv1d_triton.causal_conv1d import _fwd
 
     side = torch.cuda.Stream()
     gen = torch.Generator(device=dev).manual_seed(0)
 
     def emit(name, shape, us, fb, bb, kind, extra=None):
         line = {"config": name, "shape": shape, "pass": kind, "latency_us": round(us, 2)}
-        nbytes = fb if kind == "fwd" else fb + bb
+        nbytes = fb if kind == "fwd" else bb if kind == "bwd" else fb + bb
         if nbytes:
             line["gbs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
             line["frac_of_peak"] = round(nbytes / (us * 1e-6) / 1e9 / PEAK_GBS, 4)
@@ -340,12 +346,13 @@ def run_configs(dev, widths=False):
         return g
 
     def fwds(sets, w, b, act):
+        # Forward alone, as inference calls it: causal_conv1d_fn with autograd off.
         res = []
 
         def fn():
-            for x, _ in sets:
-                res.append(_fwd(x.detach(), w.detach(), None if b is None else b.detach(), None,
-                                None, None, act is not None))
+            with torch.no_grad():
+                for x, _ in sets:
+                    res.append(causal_conv1d_fn(x, w, b, activation=act))
         g = _capture(fn, side)
         res.clear()
         return g
@@ -358,6 +365,8 @@ def run_configs(dev, widths=False):
                 for _ in range(4)]
         b = torch.randn(D, generator=gen, device=dev).requires_grad_(True)
         for W in (2, 3, 4, 5, 6, 7, 8, 9, 12, 16):
+            if only and str(W) not in only:
+                continue
             w = (torch.randn(D, W, generator=gen, device=dev) / math.sqrt(W)).requires_grad_(True)
             fb, bb = _alg_bytes_general(B, T, D, W, True)
             shape = f"B={B} T={T} D={D} W={W} bias_silu"
@@ -367,8 +376,11 @@ def run_configs(dev, widths=False):
 
     # Configuration 2: README shape sweep, B=4 D=1024 W=4, weight only or bias + silu.
     for T in (512, 2048, 8192, 32768):
+        if not want(2, T):
+            continue
         B, D, W = 4, 1024, 4
         nsets = max(2, min(8, (512 << 20) // (2 * B * T * D * 2)))
+        nfwd = max(2, min(16, (512 << 20) // (B * T * D * 2)))
         sets = [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
                  .requires_grad_(True),
                  torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
@@ -380,10 +392,23 @@ def run_configs(dev, widths=False):
             act = "silu" if bias else None
             fb, bb = _alg_bytes_general(B, T, D, W, bias)
             shape = f"B={B} T={T} D={D} W={W} {variant}"
-            emit("2", shape, timed(fwds(sets, w, b, act), nsets), fb, bb, "fwd")
+            # forward alone over at least 512 MiB of x, twice the Infinity Cache
+            fsets = sets + [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16),
+                             None) for _ in range(max(0, nfwd - nsets))]
+            emit("2", shape, timed(fwds(fsets, w, b, act), len(fsets)), fb, bb, "fwd")
+            del fsets
             emit("2", shape, timed(steps(sets, w, b, act), nsets), fb, bb, "fwd+bwd")
         del sets
-    # Configuration 3: Mamba-2 2.7B xBC, x a channel slice of an in_proj output.
+    if want(3):
+        run_config3(dev, gen, emit, timed, steps)
+    if want(4):
+        run_config4(dev, gen, emit, timed, side)
+    if any(want(5, W) for W in (4, 7)):
+        run_config5(dev, gen, emit, timed, steps, [W for W in (4, 7) if want(5, W)])
+
+
+def run_config3(dev, gen, emit, timed, steps):
+    """Configuration 3: Mamba-2 2.7B xBC, x a channel slice of an in_proj output."""
     B, T, D, W = 8, 4096, 5376, 4
     bigs = [torch.randn(B, T, 10576, generator=gen, device=dev).to(torch.bfloat16) for _ in range(2)]
     xs = [bg[..., 5120:5120 + D].detach().requires_grad_(True) for bg in bigs]
@@ -393,9 +418,40 @@ def run_configs(dev, widths=False):
     fb, bb = _alg_bytes_general(B, T, D, W, True)
     emit("3", f"B={B} T={T} D={D} W={W} x=slice(in_proj, stride 10576)",
          timed(steps(sets, w, b, "silu", xs=xs), 2), fb, bb, "fwd+bwd")
-    del bigs, xs, sets
-    # Configuration 4: streaming, B=16 D=2048 W=4, T=8192 as 32 chunks of 256 with state handoff,
-    # and decode steps of T=1.
+    # The backward's dx into the gradient of the in_proj output: written in place through the
+    # strided-dx entry point, against a contiguous dx copied into its slice afterwards (what
+    # assembling that gradient from the slices' gradients costs).
+    from causal_conv1d_triton.causal_conv1d import _bwd
+    from causal_conv1d_triton.fused import causal_conv1d_bwd
+
+    grads = [torch.empty(B, T, 10576, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    wd, bd = w.detach(), b.detach()
+
+    def copied():
+        for (x, dy), gz in zip(sets, grads):
+            dx = _bwd(x.detach(), wd, bd, None, None, dy, None, False, True)[0]
+            gz[..., 5120:5120 + D].copy_(dx)
+
+    def in_place():
+        for (x, dy), gz in zip(sets, grads):
+            causal_conv1d_bwd(x.detach(), wd, bd, dy, dx=gz[..., 5120:5120 + D], activation="silu")
+
+    side = torch.cuda.Stream()
+    saved = 2 * B * T * D * 2
+    emit("3", f"B={B} T={T} D={D} W={W} backward, dx copied into the in_proj gradient", 
+         timed(_capture(copied, side), 2), 0, bb + saved, "bwd",
+         {"alg_bytes": bb + saved})
+    emit("3", f"B={B} T={T} D={D} W={W} backward, dx written into the in_proj gradient",
+         timed(_capture(in_place, side), 2), 0, bb, "bwd",
+         {"alg_bytes": bb, "bytes_saved_per_step": saved})
+    del bigs, xs, sets, grads
+
+
+def run_config4(dev, gen, emit, timed, side):
+    """Configuration 4: streaming, B=16 D=2048 W=4, T=8192 as 32 chunks of 256 with state
+    handoff, and decode steps of T=1."""
+    from causal_conv1d_triton import causal_conv1d_fn
+
     B, T, D, W = 16, 8192, 2048, 4
     x = torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
     w = torch.randn(D, W, generator=gen, device=dev) / 2
@@ -423,7 +479,11 @@ def run_configs(dev, widths=False):
         emit("4", f"B={B} D={D} W={W} {name} T={chunk} x{n}, state handoff", dev_us, fb, 0, "fwd",
              {"eager_us_per_call": round(host_us, 2)})
     del x
-    # Configuration 5: packed varlen seq_idx, B=4 T=16384 D=4096, W in {4, 7}, initial states.
+
+
+def run_config5(dev, gen, emit, timed, steps, widths):
+    """Configuration 5: packed varlen seq_idx, B=4 T=16384 D=4096, W in {4, 7}, initial
+    states."""
     B, T, D = 4, 16384, 4096
     seq = torch.empty(B, T, dtype=torch.int32)
     gs = torch.Generator().manual_seed(5)
@@ -435,7 +495,7 @@ def run_configs(dev, widths=False):
             t, sid = t + n, sid + 1
         seq[bb_, T - int(0.05 * T):] = -1
     seq = seq.to(dev)
-    for W in (4, 7):
+    for W in widths:
         sets = [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
                  .requires_grad_(True),
                  torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
@@ -464,6 +524,9 @@ def main():
                     help="instead of the headline line, one JSON line per BASELINE configuration 2-5")
     ap.add_argument("--widths", action="store_true",
                     help="instead of the headline line, the benchmark shape at widths 2-16")
+    ap.add_argument("--only", default="",
+                    help="with --configs or --widths: comma-separated workloads to run (e.g. "
+                         "2:512,5:7 or, with --widths, 8)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -479,7 +542,8 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     if args.configs or args.widths:
-        run_configs(dev, widths=args.widths)
+        run_configs(dev, widths=args.widths,
+                    only={t for t in args.only.split(",") if t} or None)
         return
     B, T, D, W = 4, 8192, 1024, 4
     gen = torch.Generator(device=dev).manual_seed(0)

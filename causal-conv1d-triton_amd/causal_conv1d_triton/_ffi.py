@@ -74,6 +74,9 @@ def load() -> ctypes.CDLL:
         _c_i64, _c_i64, _c_i64, _c_i64,  # batch, seqlen, dim, width
         _c_int, _c_int, _c_ptr,  # silu, device, stream
     ]
+    lib.ccv1d_fwd_inference.restype = _c_int
+    lib.ccv1d_fwd_inference.argtypes = lib.ccv1d_fwd.argtypes
+    lib.ccv1d_bwd_dx_strided.restype = _c_int
     lib.ccv1d_time_main_kernel.restype = _c_int
     lib.ccv1d_time_main_kernel.argtypes = [_c_ptr, _c_ptr]
     lib.ccv1d_bwd_workspace_bytes.restype = ctypes.c_size_t
@@ -92,6 +95,9 @@ def load() -> ctypes.CDLL:
         _c_i64, _c_i64, _c_i64, _c_i64,  # batch, seqlen, dim, width
         _c_int, _c_int, _c_ptr,  # silu, device, stream
     ]
+    lib.ccv1d_bwd_dx_strided.argtypes = (lib.ccv1d_bwd.argtypes[:16]   # x .. dx
+                                         + [_c_i64, _c_i64]             # dx strides
+                                         + lib.ccv1d_bwd.argtypes[16:])  # dinit .. stream
     lib.ccv1d_bwd_noalloc.restype = _c_int
     lib.ccv1d_bwd_noalloc.argtypes = (lib.ccv1d_bwd.argtypes[:19]   # x .. dbias, as ccv1d_bwd
                                       + lib.ccv1d_bwd.argtypes[21:])  # batch .. stream
@@ -128,7 +134,10 @@ def _stream(index: int) -> int:
     return torch.cuda.current_stream(index).cuda_stream
 
 
-def fwd(x, weight, bias, seq_idx, initial_states, out, final_states, silu: bool) -> None:
+def fwd(x, weight, bias, seq_idx, initial_states, out, final_states, silu: bool,
+        inference: bool = False) -> None:
+    """ccv1d_fwd, or with `inference` ccv1d_fwd_inference (the same kernels with the store policy
+    of a forward that no backward follows)."""
     B, T, D = x.shape
     W = weight.shape[1]
     dev = x.get_device()
@@ -142,7 +151,9 @@ def fwd(x, weight, bias, seq_idx, initial_states, out, final_states, silu: bool)
         B, T, D, W,
         int(silu), dev, _stream(dev),
     )
-    if _native is not None:
+    if inference:
+        rc = load().ccv1d_fwd_inference(*args)
+    elif _native is not None:
         rc = _native.fwd(*args)
     else:
         rc = (_lib if _lib is not None else load()).ccv1d_fwd(*args)
@@ -186,6 +197,18 @@ def _bwd_args(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx,
         dx.data_ptr(), _ptr(dinit), dweight.data_ptr(), _ptr(dbias),
     )
     return head, (B, T, D, W, int(silu), dev, _stream(dev))
+
+
+def bwd_dx_strided(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit,
+                   dweight, dbias, workspace, silu: bool) -> None:
+    """ccv1d_bwd_dx_strided through ctypes: the backward writing dx with dx's own strides."""
+    head, tail = _bwd_args(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit,
+                           dweight, dbias, silu)
+    # head ends with dx, dinit, dweight, dbias: dx's strides go right after dx
+    args = (head[:16] + (dx.stride(0), dx.stride(1)) + head[16:]
+            + (_ptr(workspace), 0 if workspace is None else workspace.numel()) + tail)
+    lib = load()
+    _check(lib.ccv1d_bwd_dx_strided(*args), lib)
 
 
 def bwd_noalloc(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit, dweight,

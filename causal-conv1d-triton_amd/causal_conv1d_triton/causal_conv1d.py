@@ -63,12 +63,13 @@ def _channels_contiguous(t: Tensor) -> Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
-def _fwd(x, weight, bias, seq_idx, initial_states, final_states, silu):
+def _fwd(x, weight, bias, seq_idx, initial_states, final_states, silu, inference=False):
     """Allocates `out` and runs the forward kernel (reference `_fwd`, causal_conv1d.py:433-472).
-    T == 0 is handled inside the library (final_states = initial_states or zeros)."""
+    T == 0 is handled inside the library (final_states = initial_states or zeros). `inference`:
+    no backward follows (the library then streams out past the caches)."""
     B, T, D = x.shape
     out = torch.empty(B, T, D, device=x.device, dtype=x.dtype)
-    _ffi.fwd(x, weight, bias, seq_idx, initial_states, out, final_states, silu)
+    _ffi.fwd(x, weight, bias, seq_idx, initial_states, out, final_states, silu, inference)
     return out
 
 
@@ -303,7 +304,7 @@ def causal_conv1d_fn(
         # Inference: no autograd node, the forward kernel writes straight into fresh buffers.
         if return_final_states:
             final_states = _new_final_states(x, weight.shape[1])
-        out = _fwd(x, weight, bias, seq_idx, initial_states, final_states, silu)
+        out = _fwd(x, weight, bias, seq_idx, initial_states, final_states, silu, inference=True)
 
     if not return_final_states:
         return out

@@ -74,6 +74,7 @@ int min_tile_rows(int64_t W) { return W < kFwdWideW ? kMinTileRows : 2 * kMinTil
 struct Tune {
   int fwd_rows = 0;
   int bwd_rows = 0;
+  int fwd_out_nt = -1;  // CCV1D_FWD_OUT_NT: 0 / 1 forces the forward's out-store policy
 };
 
 const Tune& tune() {
@@ -88,12 +89,34 @@ const Tune& tune() {
     };
     v.fwd_rows = rd("CCV1D_FWD_ROWS");
     v.bwd_rows = rd("CCV1D_BWD_ROWS");
+    if (const char* e = std::getenv("CCV1D_FWD_OUT_NT")) v.fwd_out_nt = std::atoi(e) != 0;
     return v;
   }();
 #else
   static const Tune t{};
 #endif
   return t;
+}
+
+// Bytes of x plus out above which the forward's out rows are stored non-temporally even when a
+// backward follows: half the 256 MiB Infinity Cache. Below it x stays cached for the backward, and
+// device-scope stores of out are faster (B=4 T=8192 D=1024 bf16, 128 MiB: step 60.2 us against
+// 62.8-64.2 with non-temporal stores); above it the cache cannot hold x until the backward reads it
+// and non-temporal stores win (T=32768, 512 MiB: 245-250 -> 227-231 us).
+constexpr int64_t kFwdCachedBytes = int64_t(128) << 20;
+
+// For inference (no backward follows) the threshold is lower: non-temporal out stores pay once
+// the pass streams more than 64 MiB (B=4 D=1024 bf16, forward alone: T=8192 29.6 -> 23.5-24.9 us),
+// while small calls are faster with device-scope stores (T=512: 4.24 against 4.76 us; chunks of
+// B=16 T=256 D=2048: 9.17 against 9.92 us per call).
+constexpr int64_t kFwdInferenceCachedBytes = int64_t(64) << 20;
+
+// Whether the forward stores out non-temporally, by the bytes of x and out: above
+// kFwdInferenceCachedBytes for inference, above kFwdCachedBytes when a backward follows.
+bool fwd_out_streams(bool inference, int64_t B, int64_t T, int64_t D, int x_dt) {
+  if (tune().fwd_out_nt >= 0) return tune().fwd_out_nt != 0;
+  const int64_t bytes = 2 * B * T * D * esize(x_dt);
+  return bytes > (inference ? kFwdInferenceCachedBytes : kFwdCachedBytes);
 }
 
 // Workgroups along time, per batch row and wave column, below which the tiles are shortened (down
@@ -341,11 +364,17 @@ int ccv1d_time_main_kernel(void* start_event, void* stop_event) {
   return CCV1D_OK;
 }
 
-int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+}  // extern "C"
+
+namespace {
+
+// ccv1d_fwd and ccv1d_fwd_inference: the same validation, tiling and kernels; `inference` selects
+// non-temporal out stores (fwd_out_streams).
+int fwd_entry(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
               const void* weight, int weight_dtype, const void* bias, int bias_dtype,
               const int32_t* seq_idx, const void* initial_states, int init_dtype, void* out,
               void* final_states, int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
-              int silu, int device, void* stream) {
+              int silu, int device, void* stream, bool inference) {
   g_last_error.clear();
   const bool timed = take_timing_request();
   const int64_t B = batch, T = seqlen, D = dim, W = width, P = W - 1;
@@ -405,6 +434,7 @@ int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   p.has_init = initial_states != nullptr;
   p.has_final = final_states != nullptr;
   p.silu = silu != 0;
+  p.out_nt = fwd_out_streams(inference, B, T, D, x_dtype);
   if (fast) {
     p.x_bytes = slab_bytes(x_dtype, T, D, x_stride_t);
     p.o_bytes = slab_bytes(x_dtype, T, D, D);
@@ -431,6 +461,30 @@ int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   }
   if (e != hipSuccess) return hip_fail(e, "forward launch");
   return CCV1D_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+              const void* weight, int weight_dtype, const void* bias, int bias_dtype,
+              const int32_t* seq_idx, const void* initial_states, int init_dtype, void* out,
+              void* final_states, int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+              int silu, int device, void* stream) {
+  return fwd_entry(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
+                   seq_idx, initial_states, init_dtype, out, final_states, batch, seqlen, dim,
+                   width, silu, device, stream, false);
+}
+
+int ccv1d_fwd_inference(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+                        const void* weight, int weight_dtype, const void* bias, int bias_dtype,
+                        const int32_t* seq_idx, const void* initial_states, int init_dtype,
+                        void* out, void* final_states, int64_t batch, int64_t seqlen, int64_t dim,
+                        int64_t width, int silu, int device, void* stream) {
+  return fwd_entry(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
+                   seq_idx, initial_states, init_dtype, out, final_states, batch, seqlen, dim,
+                   width, silu, device, stream, true);
 }
 
 size_t ccv1d_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
@@ -500,13 +554,14 @@ struct BwdPlan {
 
 // `ws_aligned`: the workspace the call will use is 16-byte aligned (the vectorised backward stores
 // partial rows with 16-byte accesses).
+// dx_stride_b / dx_stride_t: strides of dx in elements (T * D and D for a contiguous dx).
 int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
              const void* weight, int weight_dtype, const void* bias, int bias_dtype,
              const int32_t* seq_idx, const void* initial_states, int init_dtype,
              const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
-             const void* dfinal_states, void* dx, void* dinitial_states, void* dweight,
-             void* dbias, bool ws_aligned, int64_t batch, int64_t seqlen, int64_t dim,
-             int64_t width, int silu, BwdPlan& pl) {
+             const void* dfinal_states, void* dx, int64_t dx_stride_b, int64_t dx_stride_t,
+             void* dinitial_states, void* dweight, void* dbias, bool ws_aligned, int64_t batch,
+             int64_t seqlen, int64_t dim, int64_t width, int silu, BwdPlan& pl) {
   const int64_t B = batch, T = seqlen, D = dim, W = width;
   int rc = check_common(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
                         initial_states, init_dtype, B, T, D, W);
@@ -514,6 +569,15 @@ int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
   if (dout_stride_b < 0 || dout_stride_t < 0) return fail(CCV1D_ERR_INVALID, "negative stride");
   if (D > 0 && (T + W) * (dout_stride_t > D ? dout_stride_t : D) >= (int64_t(1) << 31))
     return fail(CCV1D_ERR_INVALID, "(seqlen + width) * max(dout time stride, dim) must be < 2^31");
+  // dx rows of one batch element must not overlap each other or the next element's.
+  if (B * T * D > 0) {
+    if ((T > 1 && dx_stride_t < D) || (B > 1 && dx_stride_b < (T - 1) * dx_stride_t + D))
+      return fail(CCV1D_ERR_INVALID, "dx strides (%lld, %lld) overlap rows of (%lld, %lld, %lld)",
+                  (long long)dx_stride_b, (long long)dx_stride_t, (long long)B, (long long)T,
+                  (long long)D);
+    if ((T + W) * (dx_stride_t > D ? dx_stride_t : D) >= (int64_t(1) << 31))
+      return fail(CCV1D_ERR_INVALID, "(seqlen + width) * max(dx time stride, dim) must be < 2^31");
+  }
   if (B * T * D > 0 && (!dout || !dx)) return fail(CCV1D_ERR_INVALID, "dout or dx is null");
   if (D > 0 && !dweight) return fail(CCV1D_ERR_INVALID, "dweight is null");
   if ((bias != nullptr) != (dbias != nullptr))
@@ -538,8 +602,10 @@ int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
   p.dinit = dinitial_states;
   p.s_xb = x_stride_b;
   p.s_yb = dout_stride_b;
+  p.s_dxb = dx_stride_b;
   p.s_xt = (int32_t)x_stride_t;
   p.s_yt = (int32_t)dout_stride_t;
+  p.s_dxt = (int32_t)dx_stride_t;
   p.B = (int32_t)B;
   p.T = (int32_t)T;
   p.D = (int32_t)D;
@@ -565,7 +631,7 @@ int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
   const int bcpl = bwd_shape(x_dtype, B, T, D, W).cpl;
   pl.fast = fast_dtype(x_dtype, W) && rows_ok(x_dtype, bcpl, T, D, x, x_stride_b, x_stride_t) &&
             rows_ok(x_dtype, bcpl, T, D, dout, dout_stride_b, dout_stride_t) &&
-            rows_ok(x_dtype, bcpl, T, D, dx, T * D, D) &&
+            rows_ok(x_dtype, bcpl, T, D, dx, dx_stride_b, dx_stride_t) &&
             (!dfinal_states || aligned_to(dfinal_states, bcpl * esize(x_dtype))) && ws_aligned;
   int64_t rows;
   if (pl.fast) {
@@ -573,7 +639,7 @@ int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
     rows = B * p.tl.nTB;
     p.x_bytes = slab_bytes(x_dtype, T, D, x_stride_t);
     p.y_bytes = slab_bytes(x_dtype, T, D, dout_stride_t);
-    p.o_bytes = slab_bytes(x_dtype, T, D, D);
+    p.o_bytes = slab_bytes(x_dtype, T, D, dx_stride_t);
   } else {
     p.tl = generic_tiling(T);
     rows = B * p.tl.nT;
@@ -661,8 +727,31 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   BwdPlan pl;
   int rc = plan_bwd(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
                     seq_idx, initial_states, init_dtype, dout, dout_stride_b, dout_stride_t,
-                    dfinal_states, dx, dinitial_states, dweight, dbias, aligned_to(workspace, 16),
-                    batch, seqlen, dim, width, silu, pl);
+                    dfinal_states, dx, seqlen * dim, dim, dinitial_states, dweight, dbias,
+                    aligned_to(workspace, 16), batch, seqlen, dim, width, silu, pl);
+  if (rc) return rc;
+  if (pl.need > 0 && (!workspace || workspace_bytes < pl.need))
+    return fail(CCV1D_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes,
+                pl.need);
+  return run_bwd(pl, workspace, device, stream, timed);
+}
+
+int ccv1d_bwd_dx_strided(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+                         const void* weight, int weight_dtype, const void* bias, int bias_dtype,
+                         const int32_t* seq_idx, const void* initial_states, int init_dtype,
+                         const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
+                         const void* dfinal_states, void* dx, int64_t dx_stride_b,
+                         int64_t dx_stride_t, void* dinitial_states, void* dweight, void* dbias,
+                         void* workspace, size_t workspace_bytes, int64_t batch, int64_t seqlen,
+                         int64_t dim, int64_t width, int silu, int device, void* stream) {
+  g_last_error.clear();
+  const bool timed = take_timing_request();
+  if (dx_stride_b < 0 || dx_stride_t < 0) return fail(CCV1D_ERR_INVALID, "negative dx stride");
+  BwdPlan pl;
+  int rc = plan_bwd(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
+                    seq_idx, initial_states, init_dtype, dout, dout_stride_b, dout_stride_t,
+                    dfinal_states, dx, dx_stride_b, dx_stride_t, dinitial_states, dweight, dbias,
+                    aligned_to(workspace, 16), batch, seqlen, dim, width, silu, pl);
   if (rc) return rc;
   if (pl.need > 0 && (!workspace || workspace_bytes < pl.need))
     return fail(CCV1D_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes,
@@ -683,8 +772,8 @@ int ccv1d_bwd_noalloc(const void* x, int64_t x_stride_b, int64_t x_stride_t, int
   // The scratch is 256-byte aligned, as the vectorised backward's partial rows require.
   int rc = plan_bwd(x, x_stride_b, x_stride_t, x_dtype, weight, weight_dtype, bias, bias_dtype,
                     seq_idx, initial_states, init_dtype, dout, dout_stride_b, dout_stride_t,
-                    dfinal_states, dx, dinitial_states, dweight, dbias, true, batch, seqlen, dim,
-                    width, silu, pl);
+                    dfinal_states, dx, seqlen * dim, dim, dinitial_states, dweight, dbias, true,
+                    batch, seqlen, dim, width, silu, pl);
   if (rc) return rc;
   if (pl.need > (size_t)CCV1D_NOALLOC_SCRATCH_BYTES)
     return fail(CCV1D_ERR_WORKSPACE,

@@ -37,6 +37,7 @@ struct FwdParams {
   int32_t B, T, D, W;
   int32_t w_dt, b_dt, i_dt;
   int32_t has_bias, has_init, has_final, silu;
+  int32_t out_nt;             // host side: non-temporal out stores for this call
   uint32_t x_bytes, o_bytes;  // per-batch byte extents of x and out (vectorised kernels)
   Tiling tl;
 };
@@ -52,12 +53,12 @@ struct BwdParams {
   void* dx;
   void* dinit;
   float* part;   // (Pn, W + 1, D) fp32 partial sums; row W holds dbias
-  int64_t s_xb, s_yb;
-  int32_t s_xt, s_yt;
+  int64_t s_xb, s_yb, s_dxb;
+  int32_t s_xt, s_yt, s_dxt;  // s_dxb, s_dxt: strides of dx (T * D and D when contiguous)
   int32_t B, T, D, W;
   int32_t w_dt, b_dt, i_dt;
   int32_t has_bias, has_init, has_dfinal, need_dinit, silu;
-  uint32_t x_bytes, y_bytes, o_bytes;  // per-batch byte extents of x, dout and dx
+  uint32_t x_bytes, y_bytes, o_bytes;  // per-batch byte extents of x, dout and dx (vectorised)
   Tiling tl;
 };
 

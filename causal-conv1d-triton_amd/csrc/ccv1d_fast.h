@@ -575,7 +575,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
   const TX* dfb = p.has_dfinal ? static_cast<const TX*>(p.dfin) + state_off : nullptr;
   const RowBuf<TX, CPL, XLD> X(static_cast<const TX*>(p.x) + (int64_t)tc.b * p.s_xb, p.x_bytes, c0, p.s_xt);
   const RowBuf<TX, CPL, YLD> Y(static_cast<const TX*>(p.dy) + (int64_t)tc.b * p.s_yb, p.y_bytes, c0, p.s_yt);
-  const RowBuf<TX, CPL, kCachePlain, DXST> DX(static_cast<const TX*>(p.dx) + (int64_t)tc.b * T * D, p.o_bytes, c0, D);
+  const RowBuf<TX, CPL, kCachePlain, DXST> DX(static_cast<const TX*>(p.dx) + (int64_t)tc.b * p.s_dxb, p.o_bytes, c0, p.s_dxt);
 
   BwdLane<TX, W, SILU, SEQ, CPL, PAD> s;
   s.own_end = own_end;

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(64) void bwd_generic_kernel(const BwdParams p) {
   xx.P = P;
   xx.D = D;
   const TX* yb = static_cast<const TX*>(p.dy) + (int64_t)b * p.s_yb + c;
-  TX* dxb = static_cast<TX*>(p.dx) + (int64_t)b * T * D + c;
+  TX* dxb = static_cast<TX*>(p.dx) + (int64_t)b * p.s_dxb + c;
   void* dinitb = need_dinit ? static_cast<char*>(p.dinit) + ((int64_t)b * P * D + c) * isz : nullptr;
   const TX* dfb = p.has_dfinal ? static_cast<const TX*>(p.dfin) + (int64_t)b * P * D + c : nullptr;
   const int32_t* sb = p.seq ? p.seq + (int64_t)b * T : nullptr;
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(64) void bwd_generic_kernel(const BwdParams p) {
       const int f = row - (T - P);
       if (f >= 0 && f < P) dx += static_cast<float>(dfb[f * D]);
     }
-    if (row >= 0) dxb[row * D] = static_cast<TX>(dx);
+    if (row >= 0) dxb[(int64_t)row * p.s_dxt] = static_cast<TX>(dx);
     else st_any(dinitb, (int64_t)(row + P) * D, p.i_dt, dx);
   };
 
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(64) void bwd_wide_kernel(const BwdParams p, const f
   xx.i_dt = p.i_dt;
   xx.P = P;
   xx.D = D;
-  TX* dxb = static_cast<TX*>(p.dx) + (int64_t)b * T * D + c;
+  TX* dxb = static_cast<TX*>(p.dx) + (int64_t)b * p.s_dxb + c;
   void* dinitb =
       p.need_dinit ? static_cast<char*>(p.dinit) + ((int64_t)b * P * D + c) * isz : nullptr;
   const TX* dfb = p.has_dfinal ? static_cast<const TX*>(p.dfin) + (int64_t)b * P * D + c : nullptr;
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(64) void bwd_wide_kernel(const BwdParams p, const f
       const int f = row - (T - P);
       if (f >= 0 && f < P) dx += static_cast<float>(dfb[(int64_t)f * D]);
     }
-    if (row >= 0) dxb[(int64_t)row * D] = static_cast<TX>(dx);
+    if (row >= 0) dxb[(int64_t)row * p.s_dxt] = static_cast<TX>(dx);
     else st_any(dinitb, (int64_t)(row + P) * D, p.i_dt, dx);
   }
 

@@ -1,7 +1,8 @@
 /* CPython extension `_ccv1d_torch`: the inference forward of causal_conv1d_fn (no autograd node)
  * in one native call. It takes torch tensors, applies the reference's argument checks and
  * canonicalisation (causal_conv1d.py:397-412, :612-617), allocates the outputs with the caching
- * allocator and calls ccv1d_fwd (include/ccv1d.h) on torch's current stream of x's device.
+ * allocator and calls ccv1d_fwd_inference (include/ccv1d.h: ccv1d_fwd's kernels with the store
+ * policy of a pass no backward follows) on torch's current stream of x's device.
  *
  * Why native: an eager decode step (batch 16, one row, state handoff) spends about 2.7 us in the
  * HIP launch and, in Python, 1.4 us reading tensor attributes, 2.6 us in two torch.empty calls and
@@ -124,7 +125,7 @@ PyObject* fwd_impl(PyObject* const* a) {
   void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev)).stream();
   int rc;
   Py_BEGIN_ALLOW_THREADS
-  rc = ccv1d_fwd(xc.data_ptr(), xc.stride(0), xc.stride(1), xdt, wc.data_ptr(), wdt,
+  rc = ccv1d_fwd_inference(xc.data_ptr(), xc.stride(0), xc.stride(1), xdt, wc.data_ptr(), wdt,
                  pb ? bc.data_ptr() : nullptr, bdt,
                  ps ? static_cast<const int32_t*>(sc.data_ptr()) : nullptr,
                  pi ? ic.data_ptr() : nullptr, idt, out.data_ptr(),

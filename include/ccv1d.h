@@ -96,6 +96,21 @@ int ccv1d_fwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
               int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
               int silu, int device, void* stream);
 
+/* Forward for inference: the arguments, results and kernels of ccv1d_fwd, for a call after which no
+ * backward reads x (no autograd). When x and out exceed 64 MiB it stores out non-temporally, which
+ * suits a pass whose input is not read again soon (ccv1d_fwd does so only above 128 MiB, half the
+ * 256 MiB Infinity Cache, and otherwise keeps both cacheable for the backward): forward alone at
+ * B=4 T=8192 D=1024 bf16, 29.6 -> about 24 us. The reference has one forward for both uses
+ * (causal_conv1d.py:433-472); results are bit-identical to ccv1d_fwd's. */
+int ccv1d_fwd_inference(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+                        const void* weight, int weight_dtype,
+                        const void* bias, int bias_dtype,
+                        const int32_t* seq_idx,
+                        const void* initial_states, int init_dtype,
+                        void* out, void* final_states,
+                        int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+                        int silu, int device, void* stream);
+
 /* Bytes of device workspace ccv1d_bwd needs for this shape: fp32 partial sums of dweight/dbias (the
  * reference allocates the same kind of buffer at causal_conv1d.py:493) and, for widths above 128,
  * an fp32 buffer of batch * seqlen * dim values for the gradient of the pre-activation. An upper
@@ -131,6 +146,29 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
               void* workspace, size_t workspace_bytes,
               int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
               int silu, int device, void* stream);
+
+/* Backward that writes dx with caller-given strides, for callers that fuse the convolution with
+ * the projection before it (the Mamba-2 in_proj epilogue): dx goes straight into its slice of the
+ * gradient of the projection's output, e.g. channels [c0, c0 + dim) of a (batch, seqlen, width_all)
+ * buffer, so no later copy assembles that gradient (which would read and write dx once more). The
+ * reference has no counterpart (its dx is always a new contiguous tensor, causal_conv1d.py:478);
+ * the CUDA causal-conv1d package's backward takes its dx buffer the same way.
+ * Arguments and results are those of ccv1d_bwd, plus dx's strides in elements (unit channel
+ * stride): dx_stride_t >= dim, dx_stride_b >= (seqlen - 1) * dx_stride_t + dim, and
+ * (seqlen + width) * max(dx_stride_t, dim) < 2^31. Elements of the buffer outside dx's rows and
+ * channels are left untouched. */
+int ccv1d_bwd_dx_strided(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
+                         const void* weight, int weight_dtype,
+                         const void* bias, int bias_dtype,
+                         const int32_t* seq_idx,
+                         const void* initial_states, int init_dtype,
+                         const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
+                         const void* dfinal_states,
+                         void* dx, int64_t dx_stride_b, int64_t dx_stride_t,
+                         void* dinitial_states, void* dweight, void* dbias,
+                         void* workspace, size_t workspace_bytes,
+                         int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
+                         int silu, int device, void* stream);
 
 /* Allocation-free backward. It has no counterpart in the reference: it is for callers that cannot
  * allocate device memory or pass a workspace (code under HIP graph capture, tight serving loops,

@@ -26,9 +26,9 @@ def _declared():
 
 
 def test_header_declares_the_entry_points():
-    assert _declared() == ["ccv1d_abi_version", "ccv1d_bwd", "ccv1d_bwd_noalloc",
-                           "ccv1d_bwd_workspace_bytes", "ccv1d_fwd", "ccv1d_last_error",
-                           "ccv1d_time_main_kernel"]
+    assert _declared() == ["ccv1d_abi_version", "ccv1d_bwd", "ccv1d_bwd_dx_strided",
+                           "ccv1d_bwd_noalloc", "ccv1d_bwd_workspace_bytes", "ccv1d_fwd",
+                           "ccv1d_fwd_inference", "ccv1d_last_error", "ccv1d_time_main_kernel"]
 
 
 def test_library_exports_every_declared_symbol():
@@ -164,6 +164,28 @@ def test_bwd_noalloc_limit_matches_workspace_sizing():
     assert limit == 32 << 20
     assert lib.ccv1d_bwd_workspace_bytes(4, 8192, 1024, 4, 2) <= limit
     assert lib.ccv1d_bwd_workspace_bytes(64, 65536, 4096, 4, 2) > limit
+
+
+def _bwd_strided(lib, dxsb, dxst, **kw):
+    a = dict(x=1 << 20, w=1 << 21, dy=1 << 22, dx=1 << 23, dw=1 << 24, B=2, T=4, D=8, W=4)
+    a.update(kw)
+    return lib.ccv1d_bwd_dx_strided(a["x"], 32, 8, 2, a["w"], 0, None, 0, None, None, 0, a["dy"],
+                                    32, 8, None, a["dx"], dxsb, dxst, None, a["dw"], None, None, 0,
+                                    a["B"], a["T"], a["D"], a["W"], 1, 0, None)
+
+
+@pytest.mark.parametrize("dxsb,dxst,msg", [
+    (32, 4, "overlap"),     # time stride below dim: rows overlap
+    (16, 8, "overlap"),     # batch stride below (T - 1) * stride + dim
+    (-1, 8, "negative"),
+    (1 << 40, 1 << 28, "2^31"),
+])
+def test_bwd_dx_strided_rejects_overlapping_or_huge_strides(dxsb, dxst, msg):
+    """Strides of dx that would make rows overlap, or in-batch offsets beyond 32 bits, are
+    refused before any HIP call."""
+    lib = _ffi.load()
+    assert _bwd_strided(lib, dxsb, dxst) == 1
+    assert msg in lib.ccv1d_last_error().decode()
 
 
 def test_timing_request_needs_both_events_or_neither():

@@ -896,3 +896,57 @@ def test_graph_replays_match_eager():
         other = step()
         torch.cuda.synchronize()
         assert torch.equal(other[2], eager[2])
+
+
+# ------------------------------------------------------------------------------------------------
+# Backward into a strided dx (fusion with the in_proj epilogue: dx lands in its slice of the
+# projection output's gradient).
+# ------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", ["aligned", "odd_offset", "generic_width", "wide_width", "seq_idx",
+                                  "states"])
+def test_backward_into_strided_dx(case):
+    """causal_conv1d_bwd writes dx into channels [c0, c0 + dim) of a wider buffer: the same bits
+    as the contiguous backward, and every other element of the buffer untouched. At an odd channel
+    offset dx's rows are not aligned for the vectorised kernels, so the generic kernels run; their
+    rounding differs from the vectorised ones', and that case is held to the tolerances."""
+    from causal_conv1d_triton.causal_conv1d import _bwd
+    from causal_conv1d_triton.fused import causal_conv1d_bwd
+
+    B, T, D, W, c0, wide = 2, 700, 512, 4, 512, 1536
+    if case == "odd_offset":
+        c0 = 3                       # rows misaligned for the vectorised kernels: generic path
+    if case == "generic_width":
+        W = 20
+    if case == "wide_width":
+        W, T, D = 200, 300, 64
+    seq = varlen_seq(31, B, T, lo=30, hi=200) if case == "seq_idx" else None
+    init = case == "states"
+    inp = make_inputs(77, B, T, D, W, init=init, seq=seq)
+    x, w, b, dy = (inp[k].to(DEV) for k in ("x", "w", "b", "dy"))
+    s0 = inp["init"].to(DEV) if init else None
+    sq = None if seq is None else seq.to(DEV)
+    dfin = inp["dfinal"].to(DEV) if case == "states" else None
+    buf = torch.full((B, T, wide), 7.0, dtype=x.dtype, device=DEV)
+    view = buf[..., c0:c0 + D]
+    dx, dw, db, dinit = causal_conv1d_bwd(x, w, b, dy, seq_idx=sq, initial_states=s0,
+                                          dfinal_states=dfin, dx=view,
+                                          return_dinitial_states=init, activation="silu")
+    want = _bwd(x, w, b, sq, s0, dy, dfin, init, True)
+    torch.cuda.synchronize()
+    assert dx.data_ptr() == view.data_ptr()
+    if case == "odd_offset":
+        torch.testing.assert_close(view.float(), want[0].float(), rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(dw, want[1], rtol=1e-3, atol=1e-3)
+        torch.testing.assert_close(db, want[2], rtol=1e-3, atol=1e-3)
+    else:
+        assert torch.equal(view, want[0]), case
+        assert torch.equal(dw, want[1]) and torch.equal(db, want[2]), case
+    if init:
+        assert torch.equal(dinit, want[3])
+    outside = torch.ones(wide, dtype=torch.bool)
+    outside[c0:c0 + D] = False
+    assert torch.all(buf[..., outside.to(DEV)] == 7.0), "elements outside dx were written"
+    ref = oracle_ref(inp, True, dfinal=dfin is not None, need_dinit=init)
+    check_lowp(dx.cpu(), ref["dx"], False, "dx")
+    check_sum(dw.cpu(), ref["dw"], "dweight")
