@@ -435,6 +435,7 @@ int fwd_entry(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   p.has_final = final_states != nullptr;
   p.silu = silu != 0;
   p.out_nt = fwd_out_streams(inference, B, T, D, x_dtype);
+  p.x_nt = inference && p.out_nt;
   if (fast) {
     p.x_bytes = slab_bytes(x_dtype, T, D, x_stride_t);
     p.o_bytes = slab_bytes(x_dtype, T, D, D);

@@ -37,7 +37,7 @@ struct FwdParams {
   int32_t B, T, D, W;
   int32_t w_dt, b_dt, i_dt;
   int32_t has_bias, has_init, has_final, silu;
-  int32_t out_nt;             // host side: non-temporal out stores for this call
+  int32_t out_nt, x_nt;       // host side: non-temporal out stores / x loads for this call
   uint32_t x_bytes, o_bytes;  // per-batch byte extents of x and out (vectorised kernels)
   Tiling tl;
 };

@@ -24,7 +24,9 @@ namespace ccv1d {
 // The forward's out stores are non-temporal instead (OST_STREAM, chosen by the host per call,
 // FwdParams::out_nt) when no backward follows (inference) and the pass streams more than 64 MiB,
 // or when x and out together exceed half the Infinity Cache, so that x would not stay resident
-// for the backward anyway: measured on
+// for the backward anyway; such inference passes also load x non-temporally (FwdParams::x_nt;
+// forward alone at B=4 T=8192 D=1024 over 512 MiB of rotating inputs 28.7 -> 27.6 us, neutral at
+// T=32768). Measured on
 // B=4 D=1024 W=4 bf16, the forward alone at T=8192 29.6 -> 23.3-24.7 us and the fwd+bwd step at
 // T=32768 245-250 -> 227-231 us, while the T=8192 step, whose 64 MiB x stays cached, is 2.7-4 us
 // faster with sc1 stores.
@@ -37,6 +39,8 @@ template <typename TX> struct FwdCfg {
   static constexpr int XLD = kCachePlain;
   static constexpr int OST = sizeof(TX) == 2 ? kCacheSC1 : kCachePlain;
   static constexpr int OST_STREAM = kCacheNT;
+  // Inference passes that stream (FwdParams::x_nt): x is read once, with no backward to find it.
+  static constexpr int XLD_STREAM = kCacheNT;
 };
 template <typename TX> struct BwdCfg {
   static constexpr int CPL = 4;
@@ -125,20 +129,21 @@ hipError_t launch_fill(void* dst, int dst_dt, const void* src, int src_dt, int64
 
 namespace ccv1d {
 
-template <typename TX, int W, bool SILU, bool SEQ, int CPL, int OST>
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int XLD, int OST>
 static hipError_t fwd_one_st(const FwdParams& p, hipStream_t s) {
   using C = FwdCfg<TX>;
   return launch(reinterpret_cast<const void*>(
-                    &fwd_fast_kernel<TX, W, SILU, SEQ, CPL, C::NW, C::R, C::XLD, OST>),
+                    &fwd_fast_kernel<TX, W, SILU, SEQ, CPL, C::NW, C::R, XLD, OST>),
                 dim3(p.tl.nBlk), dim3(C::NW * 64), 0, s, &p);
 }
 
-// The out-store policy the host chose for this call (FwdParams::out_nt).
+// The cache policies the host chose for this call (FwdParams::out_nt, x_nt; x_nt implies out_nt).
 template <typename TX, int W, bool SILU, bool SEQ, int CPL>
 static hipError_t fwd_one(const FwdParams& p, hipStream_t s) {
   using C = FwdCfg<TX>;
-  if (p.out_nt) return fwd_one_st<TX, W, SILU, SEQ, CPL, C::OST_STREAM>(p, s);
-  return fwd_one_st<TX, W, SILU, SEQ, CPL, C::OST>(p, s);
+  if (p.x_nt) return fwd_one_st<TX, W, SILU, SEQ, CPL, C::XLD_STREAM, C::OST_STREAM>(p, s);
+  if (p.out_nt) return fwd_one_st<TX, W, SILU, SEQ, CPL, C::XLD, C::OST_STREAM>(p, s);
+  return fwd_one_st<TX, W, SILU, SEQ, CPL, C::XLD, C::OST>(p, s);
 }
 
 // The channels per lane the host's tiling chose (Tiling::vec): CPL or CPL_SMALL below kFwdWideW,
