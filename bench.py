@@ -444,7 +444,26 @@ def run_config3(dev, gen, emit, timed, steps):
     emit("3", f"B={B} T={T} D={D} W={W} backward, dx written into the in_proj gradient",
          timed(_capture(in_place, side), 2), 0, bb, "bwd",
          {"alg_bytes": bb, "bytes_saved_per_step": saved})
-    del bigs, xs, sets, grads
+    del grads
+
+    # The same backward with a contiguous dx (no copy), and in place into a gradient whose rows
+    # are padded to 10624 channels (a pitch of 21248 bytes, a multiple of the 128-byte line,
+    # where Mamba's 10576 channels leave rows 32 bytes past one).
+    def contiguous():
+        for x, dy in sets:
+            _bwd(x.detach(), wd, bd, None, None, dy, None, False, True)
+
+    emit("3", f"B={B} T={T} D={D} W={W} backward, contiguous dx", timed(_capture(contiguous, side), 2),
+         0, bb, "bwd", {"alg_bytes": bb})
+    padded = [torch.empty(B, T, 10624, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+
+    def in_place_padded():
+        for (x, dy), gz in zip(sets, padded):
+            causal_conv1d_bwd(x.detach(), wd, bd, dy, dx=gz[..., 5120:5120 + D], activation="silu")
+
+    emit("3", f"B={B} T={T} D={D} W={W} backward, dx written into a gradient of 10624 channels",
+         timed(_capture(in_place_padded, side), 2), 0, bb, "bwd", {"alg_bytes": bb})
+    del bigs, xs, sets, padded
 
 
 def run_config4(dev, gen, emit, timed, side):

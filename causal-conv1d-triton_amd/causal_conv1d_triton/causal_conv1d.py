@@ -1,11 +1,9 @@
 """Causal depthwise conv1d over channels-last inputs for AMD Instinct MI355X (gfx950), with forward
-and backward:
-
-    out[b, t, d] = act(bias[d] + sum_k weight[d, k] * x[b, t - (W - 1) + k, d])
-
-where positions t < 0 read `initial_states` (or zero). x is (batch, seqlen, dim) and the states are
-(batch, width - 1, dim): the states are literally the inputs preceding x[:, 0]. Any width >= 2 and
-fp32/fp16/bf16 inputs are supported; accumulation is fp32.
+and backward. Per channel d, output row t is a dot product of the filter weight[d, 0:W] with input
+rows t-W+1 .. t (the last filter tap meets row t), plus bias[d], through an optional silu; rows
+before 0 come from `initial_states`, the W-1 rows that precede x[:, 0] (zeros without them).
+x is (batch, seqlen, dim), the states (batch, width - 1, dim). Any width >= 2; fp32, fp16 and
+bf16 inputs; fp32 arithmetic.
 
 This module is the Python side of the drop-in: it keeps the public function, autograd wiring,
 argument checks, canonicalisation and output allocation of the reference

@@ -105,10 +105,11 @@ const Tune& tune() {
 // and non-temporal stores win (T=32768, 512 MiB: 245-250 -> 227-231 us).
 constexpr int64_t kFwdCachedBytes = int64_t(128) << 20;
 
-// For inference (no backward follows) the threshold is lower: non-temporal out stores pay once
-// the pass streams more than 64 MiB (B=4 D=1024 bf16, forward alone: T=8192 29.6 -> 23.5-24.9 us),
-// while small calls are faster with device-scope stores (T=512: 4.24 against 4.76 us; chunks of
-// B=16 T=256 D=2048: 9.17 against 9.92 us per call).
+// For inference (no backward follows) the threshold is lower: non-temporal out stores, with x also
+// loaded non-temporally, pay once the pass streams more than 64 MiB (B=4 D=1024 bf16, forward
+// alone over 512 MiB of rotating x: T=8192 28.7 -> 27.4-27.6 us, T=32768 108-109 -> 105.7-106.8
+// us), while small calls are faster with the default policies (T=512: 4.24 against 4.76 us;
+// chunks of B=16 T=256 D=2048: 9.17 against 9.92 us per call).
 constexpr int64_t kFwdInferenceCachedBytes = int64_t(64) << 20;
 
 // Whether the forward stores out non-temporally, by the bytes of x and out: above

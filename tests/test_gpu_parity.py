@@ -7,8 +7,11 @@ Tolerances (from the build's north star):
     results are also required to be bit-identical to the oracle rounded to the output dtype, and
     with silu at least 99% of them must be (the exp/reciprocal implementations differ by ulps).
   * fp32 out, dx, dinit: |gpu - ref| <= 1e-5 + 1e-5 |ref|.
-  * dweight, dbias (fp32): |gpu - ref| <= 1e-3 |ref| + 1e-3 rms(ref), ref summed in double.
-    In a bf16/fp16 parameter dtype the result is rounded, so 1e-2 replaces 1e-3.
+  * dweight, dbias (fp32): |gpu - ref| <= 1e-3 |ref| + 1e-5 rms(ref), ref summed in double. The
+    absolute term covers entries near zero, where the rounding of any fp32 accumulation over the
+    rows (here and in the reference alike) is not small relative to the entry itself; over this
+    suite the largest deviation is 2.6e-6 rms(ref), and 1e-5 |ref| on entries above 0.1 rms(ref).
+    In a bf16/fp16 parameter dtype the result is rounded, so rtol 1e-2 replaces 1e-3.
   * Bit-exact: padding positions give out == 0 and dx == 0, final_states == the last width-1 rows
     of concat(initial_states, x), chunked forward == full forward, repeated backward gives the same
     dweight/dbias bits.
@@ -140,7 +143,7 @@ def check_sum(gpu, ref64, what):
     ref = torch.from_numpy(np.ascontiguousarray(ref64))
     tol = 1e-3 if gpu.dtype in (torch.float32, torch.float64) else 1e-2
     rms = ref.pow(2).mean().sqrt().item() if ref.numel() else 0.0
-    torch.testing.assert_close(gpu.double(), ref, rtol=tol, atol=tol * rms + 1e-6, msg=what)
+    torch.testing.assert_close(gpu.double(), ref, rtol=tol, atol=1e-5 * rms + 1e-7, msg=what)
 
 
 def compare(gpu, ref, silu, cols=None):
@@ -320,8 +323,7 @@ def test_seq_idx_padding_runs(W):
     assert gpu["dw"][7].isnan().any() and gpu["dw"][9].isnan().any()
     assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0)
     fin = ~gpu["dw"].isnan()
-    torch.testing.assert_close(gpu["dw"][fin], torch.from_numpy(ref["dw"]).float()[fin],
-                               rtol=1e-3, atol=1e-3)
+    check_sum(gpu["dw"][fin], ref["dw"][fin.numpy()], "dw outside the NaN channels")
 
 
 @pytest.mark.parametrize("W", [4, 7])
@@ -937,8 +939,10 @@ def test_backward_into_strided_dx(case):
     assert dx.data_ptr() == view.data_ptr()
     if case == "odd_offset":
         torch.testing.assert_close(view.float(), want[0].float(), rtol=1e-2, atol=1e-2)
-        torch.testing.assert_close(dw, want[1], rtol=1e-3, atol=1e-3)
-        torch.testing.assert_close(db, want[2], rtol=1e-3, atol=1e-3)
+        # The generic kernels sum dweight/dbias over other tiles: fp32 rounding apart.
+        for got, ref in ((dw, want[1]), (db, want[2])):
+            rms = ref.double().pow(2).mean().sqrt().item()
+            torch.testing.assert_close(got, ref, rtol=1e-3, atol=1e-5 * rms + 1e-7)
     else:
         assert torch.equal(view, want[0]), case
         assert torch.equal(dw, want[1]) and torch.equal(db, want[2]), case

@@ -115,10 +115,10 @@ def test_no_alloc_against_oracle():
     pick = lambda a: a.index_select(-1, cols.to(DEV)).float().cpu()  # noqa: E731
     torch.testing.assert_close(pick(got["dx"]), torch.from_numpy(rdx), rtol=1e-2, atol=1e-2)
     torch.testing.assert_close(pick(got["dinit"]), torch.from_numpy(rdinit), rtol=1e-2, atol=1e-2)
-    # fp32 sums against the oracle's float64 ones: rtol 1e-3, with an absolute floor of 1e-3 of
+    # fp32 sums against the oracle's float64 ones: rtol 1e-3, with an absolute floor of 1e-5 of
     # the entries' rms for sums that cancel to near zero (as in the parity tests)
     for key, ref in (("dw", rdw), ("db", rdb)):
         ref = torch.from_numpy(ref)
-        floor = 1e-3 * ref.pow(2).mean().sqrt().item()
+        floor = 1e-5 * ref.pow(2).mean().sqrt().item() + 1e-7
         torch.testing.assert_close(got[key][cols.to(DEV)].double().cpu(), ref, rtol=1e-3,
                                    atol=floor)
