@@ -554,6 +554,17 @@ struct BwdPlan {
   size_t need = 0;     // workspace bytes the launches use
 };
 
+// Bytes from the first element of a (B, T, D) array with unit channel stride to one past its last.
+int64_t span_bytes(int64_t B, int64_t T, int64_t D, int64_t s_b, int64_t s_t, int es) {
+  return ((B - 1) * s_b + (T - 1) * s_t + D) * es;
+}
+
+// Whether the byte ranges [a, a + na) and [b, b + nb) share a byte.
+bool ranges_meet(const void* a, int64_t na, const void* b, int64_t nb) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + static_cast<uintptr_t>(nb) && pb < pa + static_cast<uintptr_t>(na);
+}
+
 // `ws_aligned`: the workspace the call will use is 16-byte aligned (the vectorised backward stores
 // partial rows with 16-byte accesses).
 // dx_stride_b / dx_stride_t: strides of dx in elements (T * D and D for a contiguous dx).
@@ -581,6 +592,15 @@ int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
       return fail(CCV1D_ERR_INVALID, "(seqlen + width) * max(dx time stride, dim) must be < 2^31");
   }
   if (B * T * D > 0 && (!dout || !dx)) return fail(CCV1D_ERR_INVALID, "dout or dx is null");
+  // dx is written while the other tiles still read x and dout (halo rows): it must not share
+  // memory with either, e.g. dx = x for an in-place update.
+  if (B * T * D > 0) {
+    const int es = esize(x_dtype);
+    const int64_t ndx = span_bytes(B, T, D, dx_stride_b, dx_stride_t, es);
+    if (ranges_meet(dx, ndx, x, span_bytes(B, T, D, x_stride_b, x_stride_t, es)) ||
+        ranges_meet(dx, ndx, dout, span_bytes(B, T, D, dout_stride_b, dout_stride_t, es)))
+      return fail(CCV1D_ERR_INVALID, "dx must not overlap x or dout");
+  }
   if (D > 0 && !dweight) return fail(CCV1D_ERR_INVALID, "dweight is null");
   if ((bias != nullptr) != (dbias != nullptr))
     return fail(CCV1D_ERR_INVALID, "dbias must be given exactly when bias is");

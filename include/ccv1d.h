@@ -156,7 +156,9 @@ int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
  * Arguments and results are those of ccv1d_bwd, plus dx's strides in elements (unit channel
  * stride): dx_stride_t >= dim, dx_stride_b >= (seqlen - 1) * dx_stride_t + dim, and
  * (seqlen + width) * max(dx_stride_t, dim) < 2^31. Elements of the buffer outside dx's rows and
- * channels are left untouched. */
+ * channels are left untouched. dx must not overlap x or dout (checked on the address ranges from
+ * each one's first to its last element; CCV1D_ERR_INVALID), in this entry point and in
+ * ccv1d_bwd. */
 int ccv1d_bwd_dx_strided(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
                          const void* weight, int weight_dtype,
                          const void* bias, int bias_dtype,

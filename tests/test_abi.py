@@ -125,7 +125,8 @@ def test_bwd_rejects_invalid_arguments(kw, code, msg):
 
 
 def _bwd_noalloc(lib, **kw):
-    a = dict(x=1 << 20, xdt=2, w=1 << 21, b=None, init=None, dy=1 << 22, dfin=None, dx=1 << 23,
+    # stand-in addresses (never dereferenced) far enough apart for the largest shape below
+    a = dict(x=1 << 36, xdt=2, w=1 << 21, b=None, init=None, dy=1 << 38, dfin=None, dx=1 << 40,
              dinit=None, dw=1 << 24, db=None, B=1, T=4, D=8, W=4, seq=None)
     a.update(kw)
     return lib.ccv1d_bwd_noalloc(a["x"], 0, 8 if a["D"] == 8 else a["D"], a["xdt"], a["w"], 0,
@@ -186,6 +187,22 @@ def test_bwd_dx_strided_rejects_overlapping_or_huge_strides(dxsb, dxst, msg):
     lib = _ffi.load()
     assert _bwd_strided(lib, dxsb, dxst) == 1
     assert msg in lib.ccv1d_last_error().decode()
+
+
+@pytest.mark.parametrize("dx,dxsb,dxst", [
+    (1 << 20, 32, 8),             # dx = x: an in-place update
+    (1 << 22, 32, 8),             # dx = dout
+    ((1 << 20) + 2 * 31, 32, 8),  # dx starts at x's last element
+    ((1 << 22) - 2 * 3, 32, 8),   # dx's last row reaches into dout's first
+])
+def test_bwd_rejects_dx_overlapping_inputs(dx, dxsb, dxst):
+    """dx is written while other tiles still read x and dout: address ranges that meet are
+    refused before any HIP call (bf16: 2 bytes per element; x and dout span 32 elements)."""
+    lib = _ffi.load()
+    assert _bwd_strided(lib, dxsb, dxst, dx=dx) == 1
+    assert "overlap x or dout" in lib.ccv1d_last_error().decode()
+    assert _bwd(lib, dx=1 << 20) == 1
+    assert "overlap x or dout" in lib.ccv1d_last_error().decode()
 
 
 def test_timing_request_needs_both_events_or_neither():
