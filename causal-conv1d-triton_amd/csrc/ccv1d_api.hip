@@ -38,6 +38,17 @@ bool valid_dt(int dt) { return dt >= CCV1D_F32 && dt <= CCV1D_F64; }
 
 int esize(int dt) { return dt == CCV1D_F64 ? 8 : dt == CCV1D_F32 ? 4 : 2; }
 
+// Bytes from the first element of a (B, T, D) array with unit channel stride to one past its last.
+int64_t span_bytes(int64_t B, int64_t T, int64_t D, int64_t s_b, int64_t s_t, int es) {
+  return ((B - 1) * s_b + (T - 1) * s_t + D) * es;
+}
+
+// Whether the byte ranges [a, a + na) and [b, b + nb) share a byte.
+bool ranges_meet(const void* a, int64_t na, const void* b, int64_t nb) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + static_cast<uintptr_t>(nb) && pb < pa + static_cast<uintptr_t>(na);
+}
+
 // Channels per lane and waves per workgroup of the vectorised kernels for an x dtype.
 struct FastShape {
   int cpl, nw;
@@ -385,6 +396,11 @@ int fwd_entry(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   if (seq_idx && final_states)
     return fail(CCV1D_ERR_INVALID, "cannot return final states if seq_idx is given");
   if (B * T * D > 0 && !out) return fail(CCV1D_ERR_INVALID, "out is null");
+  // out is written while other tiles still read their halo rows of x: no in-place forward.
+  if (B * T * D > 0 &&
+      ranges_meet(out, span_bytes(B, T, D, T * D, D, esize(x_dtype)), x,
+                  span_bytes(B, T, D, x_stride_b, x_stride_t, esize(x_dtype))))
+    return fail(CCV1D_ERR_INVALID, "out must not overlap x");
   if (B * D == 0) return CCV1D_OK;
   const int fcpl = fwd_shape(x_dtype, B, T, D, W).cpl;
   const bool fast = T > 0 && fast_dtype(x_dtype, W) &&
@@ -553,17 +569,6 @@ struct BwdPlan {
   size_t g_off = 0;    // byte offset of the g buffer in the workspace (wide)
   size_t need = 0;     // workspace bytes the launches use
 };
-
-// Bytes from the first element of a (B, T, D) array with unit channel stride to one past its last.
-int64_t span_bytes(int64_t B, int64_t T, int64_t D, int64_t s_b, int64_t s_t, int es) {
-  return ((B - 1) * s_b + (T - 1) * s_t + D) * es;
-}
-
-// Whether the byte ranges [a, a + na) and [b, b + nb) share a byte.
-bool ranges_meet(const void* a, int64_t na, const void* b, int64_t nb) {
-  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
-  return pa < pb + static_cast<uintptr_t>(nb) && pb < pa + static_cast<uintptr_t>(na);
-}
 
 // `ws_aligned`: the workspace the call will use is 16-byte aligned (the vectorised backward stores
 // partial rows with 16-byte accesses).

@@ -81,7 +81,8 @@ int ccv1d_time_main_kernel(void* start_event, void* stop_event);
  *  bias              (dim,) or NULL, type bias_dtype
  *  seq_idx           (batch, seqlen) int32 or NULL
  *  initial_states    (batch, width - 1, dim) or NULL, type init_dtype
- *  out               (batch, seqlen, dim), type x_dtype
+ *  out               (batch, seqlen, dim), type x_dtype; must not overlap x (no in-place
+ *                    forward: CCV1D_ERR_INVALID)
  *  final_states      (batch, width - 1, dim) or NULL, type x_dtype: the last width - 1 rows of
  *                    concat(initial_states, x), i.e. the state for continuing the sequence. Must be
  *                    NULL when seq_idx is given (causal_conv1d.py:607-608).

@@ -83,6 +83,8 @@ def _fwd(lib, **kw):
     (dict(out=None), "out is null"),
     (dict(seq=1 << 23, fin=1 << 24), "final states"),
     (dict(T=1 << 28, D=16, sxt=16), "2^31"),
+    (dict(out=1 << 20), "overlap"),                # an in-place forward
+    (dict(out=(1 << 20) + 2 * 8 * 3), "overlap"),  # out starts at x's last row
 ])
 def test_fwd_rejects_invalid_arguments(kw, msg):
     lib = _ffi.load()
