@@ -86,6 +86,7 @@ struct Tune {
   int fwd_rows = 0;
   int bwd_rows = 0;
   int fwd_out_nt = -1;  // CCV1D_FWD_OUT_NT: 0 / 1 forces the forward's out-store policy
+  int fwd_x_nt = -1;    // CCV1D_FWD_X_NT: 1 forces non-temporal x loads (and out stores)
 };
 
 const Tune& tune() {
@@ -101,6 +102,7 @@ const Tune& tune() {
     v.fwd_rows = rd("CCV1D_FWD_ROWS");
     v.bwd_rows = rd("CCV1D_BWD_ROWS");
     if (const char* e = std::getenv("CCV1D_FWD_OUT_NT")) v.fwd_out_nt = std::atoi(e) != 0;
+    if (const char* e = std::getenv("CCV1D_FWD_X_NT")) v.fwd_x_nt = std::atoi(e) != 0;
     return v;
   }();
 #else
@@ -452,7 +454,7 @@ int fwd_entry(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   p.has_final = final_states != nullptr;
   p.silu = silu != 0;
   p.out_nt = fwd_out_streams(inference, B, T, D, x_dtype);
-  p.x_nt = inference && p.out_nt;
+  p.x_nt = tune().fwd_x_nt >= 0 ? tune().fwd_x_nt != 0 : inference && p.out_nt;
   if (fast) {
     p.x_bytes = slab_bytes(x_dtype, T, D, x_stride_t);
     p.o_bytes = slab_bytes(x_dtype, T, D, D);
