@@ -226,7 +226,7 @@ struct FwdLaneRev {
 // together; then a ping-pong over two register batches keeps batch k + 1 in flight while batch k is
 // computed. Rows past the tile end are clamped to its last row: a duplicate read keeps the number of
 // loads in flight independent of the tile length, so the compiler's wait counts stay exact.
-template <typename TX, int W, bool SILU, bool SEQ, int CPL, int R, int XLD, int OST>
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int R, int XLD, int OST, bool DRAIN>
 __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBuf<TX, CPL, XLD>& X,
                                                  const RowBuf<TX, CPL, kCachePlain, OST>& O,
                                                  const RowIds& ids, int c0, int t0, int t1,
@@ -275,6 +275,11 @@ __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBu
     for (int r = 0; r < R; ++r) O.st(t + r, s.row(buf[r], sq[r]));
   };
   int t = t0;
+  // DRAIN: wait here for every request in flight (halo, first batch, taps). The compiler's wait at
+  // the loop head merges this entry, where the first batch is the newest request, with the loop's
+  // back edge, and without this wait it waits there for everything, the previous iteration's
+  // stores included, every 2R rows; after it, the head waits only for the batch it needs.
+  if (DRAIN) __builtin_amdgcn_s_waitcnt(0);
   for (; t + 2 * R <= t1; t += 2 * R) {
     load(B, sB, t + R);
     compute(A, sA, t);
@@ -297,7 +302,7 @@ __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBu
 // One tile walked backward (outputs t1-1 down to t0), for tiles with t0 >= min_tile_rows(W) > P,
 // whose rows all lie in x. The window starts as rows t1-1-P .. t1-1; output t then takes in row t-P-1. Rows below
 // t0-P are clamped to t0-P, for the same reason as the clamp of the forward walk.
-template <typename TX, int W, bool SILU, bool SEQ, int CPL, int R, int XLD, int OST>
+template <typename TX, int W, bool SILU, bool SEQ, int CPL, int R, int XLD, int OST, bool DRAIN>
 __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBuf<TX, CPL, XLD>& X,
                                                  const RowBuf<TX, CPL, kCachePlain, OST>& O,
                                                  const RowIds& ids, int c0, int t0, int t1,
@@ -337,6 +342,7 @@ __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBu
     for (int r = 0; r < R; ++r) O.st(t - r, s.row(buf[r], sq[r]));
   };
   int t = t1 - 1;  // next output row
+  if (DRAIN) __builtin_amdgcn_s_waitcnt(0);  // as in fwd_tile_forward
   for (; t - 2 * R + 1 >= t0; t -= 2 * R) {
     load(B, sB, t - R - P - 1);
     compute(A, sA, t);
@@ -408,12 +414,23 @@ __global__ __launch_bounds__(NW * 64, (fwd_waves_per_simd<TX, W, SEQ>())) void f
     return;
   }
 
+  // The wait before the pipelined loop (DRAIN, see fwd_tile_forward) in kernels without seq_idx:
+  // B=4 D=1024 forward alone T=512 4.15 -> 4.03 us, 256-token chunks 9.40 -> 9.23, decode 2.60 ->
+  // 2.49; benchmark step 60.9 -> 60.5 us. The seq_idx kernels are 0.7 % slower with it
+  // (configuration 5), and keep the compiler's placement.
+  constexpr bool DRAIN = !SEQ;
   if (masked) {
-    if (tile & 1) fwd_tile_reverse<TX, W, SILU, SEQ, CPL, R>(p, X, O, ids, c0, t0, t1, fin);
-    else fwd_tile_forward<TX, W, SILU, SEQ, CPL, R>(p, X, O, ids, c0, t0, t1, init_off, fin);
+    if (tile & 1)
+      fwd_tile_reverse<TX, W, SILU, SEQ, CPL, R, XLD, OST, DRAIN>(p, X, O, ids, c0, t0, t1, fin);
+    else
+      fwd_tile_forward<TX, W, SILU, SEQ, CPL, R, XLD, OST, DRAIN>(p, X, O, ids, c0, t0, t1,
+                                                                  init_off, fin);
   } else {
-    if (tile & 1) fwd_tile_reverse<TX, W, SILU, false, CPL, R>(p, X, O, ids, c0, t0, t1, fin);
-    else fwd_tile_forward<TX, W, SILU, false, CPL, R>(p, X, O, ids, c0, t0, t1, init_off, fin);
+    if (tile & 1)
+      fwd_tile_reverse<TX, W, SILU, false, CPL, R, XLD, OST, DRAIN>(p, X, O, ids, c0, t0, t1, fin);
+    else
+      fwd_tile_forward<TX, W, SILU, false, CPL, R, XLD, OST, DRAIN>(p, X, O, ids, c0, t0, t1,
+                                                                    init_off, fin);
   }
 }
 
