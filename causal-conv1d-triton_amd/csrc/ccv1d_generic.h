@@ -78,11 +78,97 @@ __global__ __launch_bounds__(64) void fwd_generic_kernel(const FwdParams p) {
   }
 }
 
-// Backward, one lane per channel. The g values of the last W rows live in an LDS ring (one column
-// per lane), as do the dweight accumulators, so the width is a runtime value. Same row semantics
-// and summation structure as bwd_fast_kernel; partial row = b * nT + tile.
+// Widths up to kGenericRingW: the forward and backward below keep the weights and the window of
+// the last W rows in LDS (one column per lane), so each row of x is read from memory once and each
+// weight once per tile, instead of once per tap. The arithmetic, its order and the results are
+// those of the kernels above and below them.
+constexpr int kGenericRingW = 128;
+
+// LDS of the ring kernels, in bytes: NARR float arrays [W][64], plus the rows' sequence ids.
+__host__ __device__ constexpr size_t generic_ring_bytes(int W, int narr) {
+  return ((size_t)narr * W * 64 + W) * sizeof(float);
+}
+
+// Row slot of the ring: rows t0-P, t0-P+1, ... take slots 0, 1, ..., W-1, 0, ...
+__device__ __forceinline__ int ring_next(int s, int W) { return s + 1 == W ? 0 : s + 1; }
+
 template <typename TX>
-__global__ __launch_bounds__(64) void bwd_generic_kernel(const BwdParams p) {
+__global__ __launch_bounds__(64) void fwd_generic_ring_kernel(const FwdParams p) {
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x;
+  const int c = blockIdx.y * 64 + lane;
+  if (c >= p.D) return;
+  const int tile = blockIdx.x % p.tl.nT;
+  const int b = blockIdx.x / p.tl.nT;
+  const int T = p.T, D = p.D, W = p.W, P = W - 1;
+  const bool has_init = p.has_init;
+  const int t0 = tile * p.tl.L;
+  const int t1 = min(t0 + p.tl.L, T);
+  GenRow<TX> xx;
+  xx.xb = static_cast<const TX*>(p.x) + (int64_t)b * p.s_xb + c;
+  xx.s_xt = p.s_xt;
+  xx.initb = has_init ? static_cast<const char*>(p.init) + ((int64_t)b * P * D + c) * dt_size(p.i_dt)
+                      : nullptr;
+  xx.i_dt = p.i_dt;
+  xx.P = P;
+  xx.D = D;
+  const int32_t* sb = p.seq ? p.seq + (int64_t)b * T : nullptr;
+  float* wl = lds;                                    // weights [W][64]
+  float* xr = lds + W * 64;                           // x rows [W][64], ring
+  int32_t* sr = reinterpret_cast<int32_t*>(lds + 2 * W * 64);  // their sequence ids [W]
+  for (int k = 0; k < W; ++k) wl[k * 64 + lane] = ld_any(p.w, (int64_t)c * W + k, p.w_dt);
+  for (int q = 0; q < P; ++q) {
+    xr[q * 64 + lane] = xx(t0 - P + q);
+    if (sb) sr[q] = seq_at(sb, t0 - P + q, T, has_init);
+  }
+  const float bias = p.has_bias ? ld_any(p.bias, c, p.b_dt) : 0.0f;
+  TX* ob = static_cast<TX*>(p.out) + (int64_t)b * T * D + c;
+  int slot = P;  // slot of row t0
+  constexpr int RB = 8;
+  for (int tb = t0; tb < t1; tb += RB) {
+    // The batch's rows are requested together (rows past t1 repeat the last one).
+    float xa[RB];
+    int32_t sa[RB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int t = min(tb + i, t1 - 1);
+      xa[i] = xx(t);
+      sa[i] = sb ? sb[t] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int t = tb + i;
+      if (t >= t1) break;
+      const int32_t st = sa[i];
+      xr[slot * 64 + lane] = xa[i];
+      if (sb) sr[slot] = st;
+      // gen_conv's order: w[P] x[t], then taps k = 0 .. P-1 (rows t-P+k, slots slot+1+k mod W).
+      float z = wl[P * 64 + lane] * xa[i];
+      int s = ring_next(slot, W);
+      for (int k = 0; k < P; ++k) {
+        if (!sb || sr[s] == st) z = fmaf(wl[k * 64 + lane], xr[s * 64 + lane], z);
+        s = ring_next(s, W);
+      }
+      if (p.has_bias) z += bias;
+      if (sb && st < 0) z = 0.0f;
+      if (p.silu) z = z * sigmoid_f(z);
+      ob[(int64_t)t * D] = static_cast<TX>(z);
+      slot = ring_next(slot, W);
+    }
+  }
+  if (p.has_final && t1 == T) {
+    TX* fb = static_cast<TX*>(p.fin) + (int64_t)b * P * D + c;
+    for (int q = 0; q < P; ++q) fb[q * D] = static_cast<TX>(xx(T - P + q));
+  }
+}
+
+// Backward, one lane per channel, widths up to kGenericRingW. The last W rows of x and of g (the
+// gradient of the pre-activation) live in LDS rings that share their row slots, beside the weights
+// and the dweight sums (each a [W][64] array, one column per lane) and the rows' sequence ids; so
+// the width is a runtime value and each row of x and dout is read from memory once. Same row
+// semantics and summation structure as bwd_fast_kernel; partial row = b * nT + tile.
+template <typename TX>
+__global__ __launch_bounds__(64) void bwd_generic_ring_kernel(const BwdParams p) {
   extern __shared__ float lds[];
   const int lane = threadIdx.x;
   const int c = blockIdx.y * 64 + lane;
@@ -93,11 +179,16 @@ __global__ __launch_bounds__(64) void bwd_generic_kernel(const BwdParams p) {
   const bool has_init = p.has_init;
   const bool silu = p.silu;
   const bool need_dinit = p.need_dinit;
-  float* gring = lds;            // [W][64]: g of rows t-P .. t, slot = row mod W
-  float* dwl = lds + W * 64;     // [W][64]: dweight accumulators
+  float* wl = lds;                                    // weights [W][64]
+  float* xr = lds + W * 64;                           // x rows [W][64], ring
+  float* gr = lds + 2 * W * 64;                       // g rows [W][64], same slots
+  float* dwl = lds + 3 * W * 64;                      // dweight sums [W][64]
+  int32_t* sr = reinterpret_cast<int32_t*>(lds + 4 * W * 64);  // the rows' sequence ids [W]
+  const int64_t wo = (int64_t)c * W;
   for (int k = 0; k < W; ++k) {
-    gring[k * 64 + lane] = 0.0f;
+    wl[k * 64 + lane] = ld_any(p.w, wo + k, p.w_dt);
     dwl[k * 64 + lane] = 0.0f;
+    gr[k * 64 + lane] = 0.0f;
   }
   float db = 0.0f;
 
@@ -115,21 +206,24 @@ __global__ __launch_bounds__(64) void bwd_generic_kernel(const BwdParams p) {
   const TX* dfb = p.has_dfinal ? static_cast<const TX*>(p.dfin) + (int64_t)b * P * D + c : nullptr;
   const int32_t* sb = p.seq ? p.seq + (int64_t)b * T : nullptr;
   const float bias = p.has_bias ? ld_any(p.bias, c, p.b_dt) : 0.0f;
-  const int64_t wo = (int64_t)c * W;
 
   const int t0 = tile * p.tl.L;
   const int own_end = min(t0 + p.tl.L, T);
   const int t_end = min(own_end + P, T);
   const int emit_lo = (tile == 0 && need_dinit) ? -P : t0;
-  auto slot = [&](int row) { return ((row % W) + W) % W; };
+  for (int q = 0; q < P; ++q) {
+    xr[q * 64 + lane] = xx(t0 - P + q);
+    if (sb) sr[q] = seq_at(sb, t0 - P + q, T, has_init);
+  }
 
-  // dx of `row` from the g ring (rows row .. row + P), plus dfinal; stores dx or dinit.
-  auto emit = [&](int row) {
-    const int32_t s0 = sb ? seq_at(sb, row, T, has_init) : 0;
-    float dx = ld_any(p.w, wo + P, p.w_dt) * gring[slot(row) * 64 + lane];
+  // dx of `row` (slot `s0`; rows row .. row + P in the ring), plus dfinal; stores dx or dinit.
+  auto emit = [&](int row, int s0) {
+    const int32_t q0 = sb ? sr[s0] : 0;
+    float dx = wl[P * 64 + lane] * gr[s0 * 64 + lane];
+    int s = ring_next(s0, W);
     for (int j = 1; j <= P; ++j) {
-      if (sb && seq_at(sb, row + j, T, has_init) != s0) continue;
-      dx = fmaf(ld_any(p.w, wo + P - j, p.w_dt), gring[slot(row + j) * 64 + lane], dx);
+      if (!sb || sr[s] == q0) dx = fmaf(wl[(P - j) * 64 + lane], gr[s * 64 + lane], dx);
+      s = ring_next(s, W);
     }
     if (dfb) {
       const int f = row - (T - P);
@@ -139,32 +233,60 @@ __global__ __launch_bounds__(64) void bwd_generic_kernel(const BwdParams p) {
     else st_any(dinitb, (int64_t)(row + P) * D, p.i_dt, dx);
   };
 
-  for (int tt = t0; tt < t_end; ++tt) {
-    const int32_t st = sb ? sb[tt] : 0;
-    float g = static_cast<float>(yb[tt * p.s_yt]);
-    if (silu) {
-      float z = gen_conv(xx, p.w, p.w_dt, c, W, sb, T, has_init, tt, st);
-      if (p.has_bias) z += bias;
-      g = dsilu_times(g, z);
+  int slot = P;  // slot of row tt
+  constexpr int RB = 8;
+  for (int tb = t0; tb < t_end; tb += RB) {
+    float xa[RB], ya[RB];
+    int32_t sa[RB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int t = min(tb + i, t_end - 1);
+      xa[i] = xx(t);
+      ya[i] = static_cast<float>(yb[(int64_t)t * p.s_yt]);
+      sa[i] = sb ? sb[t] : 0;
     }
-    if (sb && st < 0) g = 0.0f;
-    gring[slot(tt) * 64 + lane] = g;
-    if (tt < own_end) {
-      for (int k = 0; k < P; ++k) {
-        const int r = tt - P + k;
-        if (sb && seq_at(sb, r, T, has_init) != st) continue;
-        dwl[k * 64 + lane] = fmaf(g, xx(r), dwl[k * 64 + lane]);
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int tt = tb + i;
+      if (tt >= t_end) break;
+      const int32_t st = sa[i];
+      xr[slot * 64 + lane] = xa[i];
+      if (sb) sr[slot] = st;
+      float g = ya[i];
+      if (silu) {
+        float z = wl[P * 64 + lane] * xa[i];
+        int s = ring_next(slot, W);
+        for (int k = 0; k < P; ++k) {
+          if (!sb || sr[s] == st) z = fmaf(wl[k * 64 + lane], xr[s * 64 + lane], z);
+          s = ring_next(s, W);
+        }
+        if (p.has_bias) z += bias;
+        g = dsilu_times(g, z);
       }
-      dwl[P * 64 + lane] = fmaf(g, xx(tt), dwl[P * 64 + lane]);
-      db += g;
+      if (sb && st < 0) g = 0.0f;
+      gr[slot * 64 + lane] = g;
+      if (tt < own_end) {
+        int s = ring_next(slot, W);
+        for (int k = 0; k < P; ++k) {
+          if (!sb || sr[s] == st) dwl[k * 64 + lane] = fmaf(g, xr[s * 64 + lane], dwl[k * 64 + lane]);
+          s = ring_next(s, W);
+        }
+        dwl[P * 64 + lane] = fmaf(g, xa[i], dwl[P * 64 + lane]);
+        db += g;
+      }
+      // Row tt - P sits in the slot after tt's.
+      if (tt - P >= emit_lo) emit(tt - P, ring_next(slot, W));
+      slot = ring_next(slot, W);
     }
-    if (tt - P >= emit_lo) emit(tt - P);
   }
   if (t_end == T) {
+    // Rows past the end: g = 0 and sequence id -1.
     for (int q = 0; q < P; ++q) {
-      gring[slot(T + q) * 64 + lane] = 0.0f;
+      gr[slot * 64 + lane] = 0.0f;
+      if (sb) sr[slot] = -1;
       const int row = T + q - P;
-      if (row >= emit_lo && row < own_end) emit(row);
+      if (row >= emit_lo && row < own_end) emit(row, ring_next(slot, W));
+      slot = ring_next(slot, W);
     }
   }
 

@@ -5,17 +5,37 @@
 
 namespace ccv1d {
 
-template <typename TX>
-hipError_t launch_fwd_generic_t(const FwdParams& p, hipStream_t s) {
-  const dim3 grid((unsigned)((int64_t)p.B * p.tl.nT), (unsigned)((p.D + 63) / 64));
-  return launch(reinterpret_cast<const void*>(&fwd_generic_kernel<TX>), grid, dim3(64), 0, s, &p);
+static_assert(kMaxGenericW <= kGenericRingW, "the ring backward covers every generic width");
+static_assert(generic_ring_bytes(kGenericRingW, 4) <= 160 * 1024, "LDS of one gfx950 CU");
+
+// Dynamic LDS above the default 64 KiB per workgroup must be allowed per kernel first.
+static hipError_t allow_lds(const void* kernel, size_t bytes) {
+  if (bytes <= 65536) return hipSuccess;
+  return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
 template <typename TX>
+hipError_t launch_fwd_generic_t(const FwdParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)((int64_t)p.B * p.tl.nT), (unsigned)((p.D + 63) / 64));
+  if (p.W <= kGenericRingW) {
+    const void* k = reinterpret_cast<const void*>(&fwd_generic_ring_kernel<TX>);
+    const size_t shmem = generic_ring_bytes(p.W, 2);
+    const hipError_t e = allow_lds(k, shmem);
+    if (e != hipSuccess) return e;
+    return launch(k, grid, dim3(64), shmem, s, &p);
+  }
+  return launch(reinterpret_cast<const void*>(&fwd_generic_kernel<TX>), grid, dim3(64), 0, s, &p);
+}
+
+// Widths up to kMaxGenericW (<= kGenericRingW); wider ones take launch_bwd_wide_t.
+template <typename TX>
 hipError_t launch_bwd_generic_t(const BwdParams& p, hipStream_t s) {
   const dim3 grid((unsigned)((int64_t)p.B * p.tl.nT), (unsigned)((p.D + 63) / 64));
-  const size_t shmem = (size_t)2 * p.W * 64 * sizeof(float);
-  return launch(reinterpret_cast<const void*>(&bwd_generic_kernel<TX>), grid, dim3(64), shmem, s, &p);
+  const void* k = reinterpret_cast<const void*>(&bwd_generic_ring_kernel<TX>);
+  const size_t shmem = generic_ring_bytes(p.W, 4);
+  const hipError_t e = allow_lds(k, shmem);
+  if (e != hipSuccess) return e;
+  return launch(k, grid, dim3(64), shmem, s, &p);
 }
 
 template <typename TX>

@@ -58,8 +58,9 @@ template <typename TX> struct BwdCfg {
 constexpr int kMaxFastW = 16;    // widths 2..kMaxFastW have register-window kernels
 constexpr int kFwdWideW = 9;     // first width whose forward always uses FwdCfg::CPL_SMALL
 constexpr int kBwdWideW = 6;     // first width whose backward uses BwdCfg::CPL_WIDE
-constexpr int kMaxGenericW = 128;  // LDS ring of the generic backward: 2 * W * 64 * 4 bytes; wider
-                                   // backwards keep g in the workspace (bwd_g/bwd_wide kernels)
+constexpr int kMaxGenericW = 128;  // LDS rings of the generic backward (x, g, weights, dweight
+                                   // sums: 4 * W * 64 * 4 bytes + the rows' ids, 128.5 KiB at 128);
+                                   // wider backwards keep g in the workspace (bwd_g/bwd_wide)
 constexpr int kReduceNW = 16;    // waves per reduction workgroup
 constexpr int kGenericL = 64;    // rows per tile of the generic kernels
 
