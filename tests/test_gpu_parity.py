@@ -581,6 +581,27 @@ def test_empty_inputs(shape):
         assert torch.equal(init.grad, dfin.to(init.dtype))
 
 
+@pytest.mark.parametrize("W", [17, 64, 100, 128])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+def test_generic_ring_widths(W, xdt):
+    """Widths 17-128 run the generic kernels with their weights and row windows in LDS; from width
+    64 the backward's LDS exceeds the default 64 KiB and the launcher raises the kernel's limit.
+    Against the oracle around the window length, with initial and final states and their
+    gradients, and with seq_idx."""
+    D = 72
+    for T in (1, W - 1, W + 1, 300):
+        init = T % 2 == 1
+        inp = make_inputs(3 * W + T, 2, T, D, W, xdt=xdt, init=init)
+        gpu = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=init)
+        ref = oracle_ref(inp, True, final=True, dfinal=True, need_dinit=init)
+        compare(gpu, ref, True)
+    seq = varlen_seq(W, 2, 400, lo=20, hi=150, pad_frac=0.1)
+    inp = make_inputs(5 * W, 2, 400, D, W, xdt=xdt, init=True, seq=seq)
+    gpu = run_gpu(inp, "silu", init_grad=True)
+    compare(gpu, oracle_ref(inp, True, need_dinit=True), True)
+    assert torch.all(gpu["out"][seq < 0] == 0) and torch.all(gpu["dx"][seq < 0] == 0)
+
+
 @pytest.mark.parametrize("W", [129, 200, 257])
 @pytest.mark.parametrize("D", [8, 100])
 def test_widths_above_128(W, D):
