@@ -581,6 +581,40 @@ def test_empty_inputs(shape):
         assert torch.equal(init.grad, dfin.to(init.dtype))
 
 
+@pytest.mark.parametrize("case", ["cached", "seq_states", "streamed"])
+def test_forward_cache_policies_leave_results_unchanged(case):
+    """The forward picks its load/store cache policies and, for streaming inference calls, its
+    workgroup walk per call (inference or training, and the bytes of x and out against the
+    Infinity Cache); none of it touches the arithmetic. A training forward and an inference forward
+    of the same inputs give identical outputs bit for bit, on both sides of the thresholds (64 MiB
+    for inference, 128 MiB for training), and a channel subset matches the oracle."""
+    B, T, D, W = {"cached": (4, 8192, 1024, 4), "seq_states": (2, 16384, 2048, 4),
+                  "streamed": (4, 16384, 1024, 7)}[case]
+    seq = varlen_seq(17, B, T, lo=64, hi=4096) if case == "seq_states" else None
+    inp = make_inputs(41, B, T, D, W, init=case == "seq_states", seq=seq)
+    x, w, b = inp["x"].to(DEV), inp["w"].to(DEV), inp["b"].to(DEV)
+    init = None if inp["init"] is None else inp["init"].to(DEV)
+    sq = None if seq is None else seq.to(DEV)
+    final = seq is None
+    xg = x.clone().requires_grad_(True)
+    trained = causal_conv1d_fn(xg, w, b, seq_idx=sq, initial_states=init,
+                               return_final_states=final, activation="silu")
+    with torch.no_grad():
+        inferred = causal_conv1d_fn(x, w, b, seq_idx=sq, initial_states=init,
+                                    return_final_states=final, activation="silu")
+    torch.cuda.synchronize()
+    if final:
+        assert torch.equal(trained[0].detach(), inferred[0])
+        assert torch.equal(trained[1].detach(), inferred[1])
+        out = inferred[0]
+    else:
+        assert torch.equal(trained.detach(), inferred)
+        out = inferred
+    cols = _cols(D, 6, 43)
+    ref = oracle_ref(inp, True, cols=cols, bwd=False)
+    check_lowp(_sub(out.cpu(), cols), ref["out"], False, "out")
+
+
 @pytest.mark.parametrize("W", [17, 64, 100, 128])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
 def test_generic_ring_widths(W, xdt):
