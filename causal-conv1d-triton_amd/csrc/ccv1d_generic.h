@@ -298,7 +298,7 @@ __global__ __launch_bounds__(64) void bwd_generic_ring_kernel(const BwdParams p)
 // Backward for widths whose g ring would not fit LDS (above kMaxGenericW): the gradient g of the
 // pre-activation goes to a fp32 buffer G (batch, seqlen, dim) in the workspace, and a second kernel
 // forms dx and the dweight/dbias partial rows from it, so no on-chip storage grows with the width.
-// Same row semantics, summation orders and partial-row layout as bwd_generic_kernel.
+// Same row semantics, summation orders and partial-row layout as bwd_generic_ring_kernel.
 
 // G[b, t, c] = dout * silu'(z) (or dout), 0 on padding rows (causal_conv1d.py:274-288).
 template <typename TX>
