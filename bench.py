@@ -304,7 +304,7 @@ def run_configs(dev, widths=False, only=None):
     call from replayed graphs after the usual warm-up, plus, for the latency-bound streaming and
     decode calls, the host-inclusive eager time per call. With `widths`, instead: the benchmark
     shape (bf16, bias + silu) at every width the vectorised kernels cover, forward alone and
-    forward + backward (widths 2-8, 9, 12 and 16).
+    forward + backward (widths 2-8, 9, 12, 16, 17, 20, 24 and 32).
 
     `only` (a set of strings, e.g. {"2:512", "5:7"} or, with `widths`, {"8"}) restricts the run to
     the named configurations (N, or N:T for configuration 2's lengths, N:W for configuration 5's
@@ -364,7 +364,7 @@ def run_configs(dev, widths=False, only=None):
                  torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
                 for _ in range(4)]
         b = torch.randn(D, generator=gen, device=dev).requires_grad_(True)
-        for W in (2, 3, 4, 5, 6, 7, 8, 9, 12, 16):
+        for W in (2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 17, 20, 24, 32):
             if only and str(W) not in only:
                 continue
             w = (torch.randn(D, W, generator=gen, device=dev) / math.sqrt(W)).requires_grad_(True)
@@ -542,7 +542,7 @@ def main():
     ap.add_argument("--configs", action="store_true",
                     help="instead of the headline line, one JSON line per BASELINE configuration 2-5")
     ap.add_argument("--widths", action="store_true",
-                    help="instead of the headline line, the benchmark shape at widths 2-16")
+                    help="instead of the headline line, the benchmark shape at widths 2-32")
     ap.add_argument("--only", default="",
                     help="with --configs or --widths: comma-separated workloads to run (e.g. "
                          "2:512,5:7 or, with --widths, 8)")

@@ -70,11 +70,15 @@ FastShape shape_of(int x_dt) {
 constexpr int kMaxTileRows = 64;
 constexpr int kMinTileRows = 8;
 static_assert(kMaxTileRows + 2 * (kMaxFastW - 1) <= kRowIds, "tile and halos must fit one RowIds");
-static_assert(kMinTileRows > kFwdWideW - 2 && 2 * kMinTileRows > kMaxFastW - 1,
-              "a tile must be longer than the window");
+static_assert(kMaxFastW <= kMaxTileRows, "the longest tile must be longer than every window");
 
-// Shortest tile for width W: kMinTileRows, doubled from width kFwdWideW up.
-int min_tile_rows(int64_t W) { return W < kFwdWideW ? kMinTileRows : 2 * kMinTileRows; }
+// Shortest tile for width W: the shortest power of two from kMinTileRows up that is longer than the
+// window of W - 1 rows (8 rows up to width 8, 16 up to 16, 32 up to 32).
+int min_tile_rows(int64_t W) {
+  int L = kMinTileRows;
+  while (L < W) L *= 2;
+  return L;
+}
 
 // Row tiling overrides for tuning sweeps: CCV1D_FWD_ROWS / CCV1D_BWD_ROWS (rows per tile of the
 // vectorised kernels; a power of two in [8, kMaxTileRows], ignored for widths whose shortest tile
@@ -176,7 +180,7 @@ constexpr int64_t kFwdSmallGrid = 256;
 Tiling fwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw) {
   const int lmin = min_tile_rows(W);
   const int over = tune().fwd_rows >= lmin ? tune().fwd_rows : 0;
-  Tiling t = fast_tiling(B, T, D, cpl, nw, 16, kMaxTileRows, kTargetWaves, over);
+  Tiling t = fast_tiling(B, T, D, cpl, nw, lmin > 16 ? lmin : 16, kMaxTileRows, kTargetWaves, over);
   if (over == 0 && t.L == 16 && lmin < 16 && t.nBlk < kFwdSmallGrid)
     t = fast_tiling(B, T, D, cpl, nw, lmin, lmin, kTargetWaves, lmin);
   return t;
@@ -197,10 +201,13 @@ int fwd_cpl_small(int x_dt) {
 // per call, decode steps 2.56 -> 2.53. Grids that reach the target keep 4 channels (benchmark shape
 // 29.5 against 31.8 us; B=2 T=8192 D=1024 13.3 against 14.0). fp32 x follows the same rule in both
 // passes (fwd+bwd step, B=4 D=1024 W=4: T=512 19.1 -> 16.8 us, T=2048 39.9 -> 37.7). From width
-// kFwdWideW up the forward always takes CPL_SMALL (its weights and window are per channel).
+// kFwdWideW up the forward always takes CPL_SMALL (its weights and window are per channel), from
+// kFwdLongW up kCplLong.
 FastShape fwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
   FastShape sh = shape_of<FwdCfg>(x_dt);
-  if (W >= kFwdWideW) {
+  if (W >= kFwdLongW) {
+    sh.cpl = kCplLong;
+  } else if (W >= kFwdWideW) {
     sh.cpl = fwd_cpl_small(x_dt);
   } else if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
     const Tiling t = fwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);
@@ -251,10 +258,12 @@ int cpl_wide(int x_dt) {
 
 // Channels per lane and waves per workgroup of the vectorised backward for a shape: CPL_WIDE from
 // kBwdWideW up (register budget), and below it when the 4-channel grid is small (above) or dim is
-// not a multiple of 4; CPL otherwise.
+// not a multiple of 4; CPL otherwise; kCplLong from kBwdLongW up.
 FastShape bwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
   FastShape sh = shape_of<BwdCfg>(x_dt);
-  if (W >= kBwdWideW) {
+  if (W >= kBwdLongW) {
+    sh.cpl = kCplLong;
+  } else if (W >= kBwdWideW) {
     sh.cpl = cpl_wide(x_dt);
   } else if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
     const Tiling t = bwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);

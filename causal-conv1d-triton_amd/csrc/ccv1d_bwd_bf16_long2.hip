@@ -1,0 +1,8 @@
+// Instantiations of the vectorised bwd kernels for x of type __bf16 (widths 25..32, one channel per
+// lane, with and without silu and seq_idx).
+#define CCV1D_DEFINE_FAST_LAUNCHERS
+#include "ccv1d_launch.h"
+
+namespace ccv1d {
+template hipError_t launch_bwd_fast_long2_t<__bf16>(const BwdParams& p, hipStream_t s);
+}  // namespace ccv1d

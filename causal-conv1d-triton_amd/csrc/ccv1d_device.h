@@ -95,7 +95,7 @@ __device__ __forceinline__ void st_any(void* p, int64_t i, int dt, float v) {
 
 // ---------------------------------------------------------------------------------------------
 // Channel vectors of the x dtype. One lane moves CPL consecutive channels of one row with a single
-// 4-, 8- or 16-byte load or store, so a wave covers 64 * CPL channels (256 B to 1 KiB) per
+// 2-, 4-, 8- or 16-byte load or store, so a wave covers 64 * CPL channels (128 B to 1 KiB) per
 // instruction.
 // ---------------------------------------------------------------------------------------------
 
@@ -107,6 +107,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int BYTES> struct RawOf;
+template <> struct RawOf<2> { using type = uint16_t; };
 template <> struct RawOf<4> { using type = u32x1; };
 template <> struct RawOf<8> { using type = u32x2; };
 template <> struct RawOf<16> { using type = u32x4; };
@@ -125,38 +126,47 @@ struct VecIO {
   }
 
   __device__ static __forceinline__ void unpack(const raw v, float (&f)[CPL]) {
+    if constexpr (BYTES == 2) {  // one 16-bit channel
+      if constexpr (__is_same(TX, __bf16)) f[0] = __uint_as_float((uint32_t)v << 16);
+      else f[0] = static_cast<float>(__builtin_bit_cast(_Float16, v));
+    } else {
 #pragma unroll
-    for (int j = 0; j < WORDS; ++j) {
-      const uint32_t u = v[j];
-      if constexpr (sizeof(TX) == 4) {
-        f[j] = __uint_as_float(u);
-      } else if constexpr (__is_same(TX, __bf16)) {
-        f[2 * j] = __uint_as_float(u << 16);
-        f[2 * j + 1] = __uint_as_float(u & 0xffff0000u);
-      } else {
-        const f2v q = __builtin_convertvector(__builtin_bit_cast(h2v, u), f2v);
-        f[2 * j] = q.x;
-        f[2 * j + 1] = q.y;
+      for (int j = 0; j < WORDS; ++j) {
+        const uint32_t u = v[j];
+        if constexpr (sizeof(TX) == 4) {
+          f[j] = __uint_as_float(u);
+        } else if constexpr (__is_same(TX, __bf16)) {
+          f[2 * j] = __uint_as_float(u << 16);
+          f[2 * j + 1] = __uint_as_float(u & 0xffff0000u);
+        } else {
+          const f2v q = __builtin_convertvector(__builtin_bit_cast(h2v, u), f2v);
+          f[2 * j] = q.x;
+          f[2 * j + 1] = q.y;
+        }
       }
     }
   }
 
   // Round-to-nearest-even; one v_cvt_pk_{bf16,f16}_f32 per channel pair.
   __device__ static __forceinline__ raw pack(const float (&f)[CPL]) {
-    raw v;
+    if constexpr (BYTES == 2) {
+      return __builtin_bit_cast(raw, static_cast<TX>(f[0]));
+    } else {
+      raw v;
 #pragma unroll
-    for (int j = 0; j < WORDS; ++j) {
-      if constexpr (sizeof(TX) == 4) {
-        v[j] = __float_as_uint(f[j]);
-      } else if constexpr (__is_same(TX, __bf16)) {
-        v[j] = __builtin_bit_cast(uint32_t,
-                                  __builtin_convertvector((f2v){f[2 * j], f[2 * j + 1]}, bf2v));
-      } else {
-        v[j] = __builtin_bit_cast(uint32_t,
-                                  __builtin_convertvector((f2v){f[2 * j], f[2 * j + 1]}, h2v));
+      for (int j = 0; j < WORDS; ++j) {
+        if constexpr (sizeof(TX) == 4) {
+          v[j] = __float_as_uint(f[j]);
+        } else if constexpr (__is_same(TX, __bf16)) {
+          v[j] = __builtin_bit_cast(uint32_t,
+                                    __builtin_convertvector((f2v){f[2 * j], f[2 * j + 1]}, bf2v));
+        } else {
+          v[j] = __builtin_bit_cast(uint32_t,
+                                    __builtin_convertvector((f2v){f[2 * j], f[2 * j + 1]}, h2v));
+        }
       }
+      return v;
     }
-    return v;
   }
 };
 
@@ -201,8 +211,10 @@ struct RowBuf {
       return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, (uint32_t)row * row_bytes, LD));
     else if constexpr (IO::BYTES == 8)
       return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b64(rs, lane_off, (uint32_t)row * row_bytes, LD));
-    else
+    else if constexpr (IO::BYTES == 4)
       return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b32(rs, lane_off, (uint32_t)row * row_bytes, LD));
+    else
+      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b16(rs, lane_off, (uint32_t)row * row_bytes, LD));
   }
   __device__ __forceinline__ void st(int row, raw v) const {
     if constexpr (IO::BYTES == 16) {
@@ -213,9 +225,11 @@ struct RowBuf {
     } else if constexpr (IO::BYTES == 8) {
       __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), rs, lane_off,
                                             (uint32_t)row * row_bytes, ST);
-    } else {
+    } else if constexpr (IO::BYTES == 4) {
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rs, lane_off,
                                             (uint32_t)row * row_bytes, ST);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b16(v, rs, lane_off, (uint32_t)row * row_bytes, ST);
     }
   }
 };

@@ -1,5 +1,5 @@
-// Vectorised forward and backward kernels for compile-time widths (2..kMaxFastW = 16) and
-// channels-last x whose rows are aligned to the 4-, 8- or 16-byte access of CPL channels.
+// Vectorised forward and backward kernels for compile-time widths (2..kMaxFastW = 32) and
+// channels-last x whose rows are aligned to the 2-, 4-, 8- or 16-byte access of CPL channels.
 //
 // Work decomposition (both passes): a lane owns CPL consecutive channels, a wave owns 64 such
 // channel vectors over a tile of L consecutive rows, and a workgroup holds NW waves on consecutive
@@ -111,7 +111,7 @@ struct TileCoord {
 
 // Sequence ids of rows r0 .. r0 + 127 of concat(initial_states, x) (kRowIds rows), row r0 + j in
 // lane j of `lo` (j < 64) or lane j - 64 of `hi`, read with two vector loads issued together. A tile
-// and both its halos span at most 64 + 2 * 15 rows, so one RowIds serves every row a tile touches:
+// and both its halos span at most 64 + 2 * 31 rows, so one RowIds serves every row a tile touches:
 // at() gives the id of a row to the whole wave (v_readlane) without a load of its own, and no load
 // of ids then sits in the tile's pipelined loop, where its wait would also cover the loads and
 // stores issued before it.

@@ -1,4 +1,4 @@
-// Scalar kernels for what the vectorised path does not cover: widths above kMaxFastW (16), channel
+// Scalar kernels for what the vectorised path does not cover: widths above kMaxFastW (32), channel
 // counts that are not a multiple of the channels per lane, rows not aligned to the vector access,
 // and fp64 x. One lane
 // owns one channel of one tile; the lanes of a wave cover 64 consecutive channels, so every row

@@ -44,7 +44,7 @@ template <typename TX> struct FwdCfg {
 };
 template <typename TX> struct BwdCfg {
   static constexpr int CPL = 4;
-  // Widths from kBwdWideW up keep 2 channels per lane: 4 would need about 150-190 VGPRs (the
+  // Widths kBwdWideW..kBwdLongW-1 keep 2 channels per lane: 4 would need about 150-190 VGPRs (the
   // weights, the x and g windows and the dweight sums are all per channel), one workgroup per CU;
   // with 2 the kernel holds 4 waves per SIMD (B=4 T=16384 D=4096 W=7 with seq_idx: 657 -> 582 us
   // per step; at W=4 the benchmark shape is 2.5 us faster with 4 channels).
@@ -55,9 +55,21 @@ template <typename TX> struct BwdCfg {
   static constexpr int YLD = kCacheNT;
   static constexpr int DXST = sizeof(TX) == 2 ? kCacheSC1NT : kCacheNT;
 };
-constexpr int kMaxFastW = 16;    // widths 2..kMaxFastW have register-window kernels
+constexpr int kMaxFastW = 32;    // widths 2..kMaxFastW have register-window kernels
 constexpr int kFwdWideW = 9;     // first width whose forward always uses FwdCfg::CPL_SMALL
 constexpr int kBwdWideW = 6;     // first width whose backward uses BwdCfg::CPL_WIDE
+// One channel per lane (kCplLong) from width kFwdLongW in the forward and from kBwdLongW in the
+// backward. From width 17 the weights, the windows and the dweight sums of W taps per channel fit
+// the registers of 2 waves per SIMD only with one channel (backward at width 32: 187-189 VGPRs,
+// no spills). The backward takes one channel from width 11 already: 80-112 VGPRs at widths 11-16
+// (4-6 waves per SIMD, against 2 with two channels). Measured (bf16, B=4 T=8192 D=1024, bias +
+// silu, fwd+bwd step, 2 against 1 channel in the backward): W=11 84.0 -> 80.7 us, W=12 86.0 ->
+// 82.2, W=14 94.8 -> 90.5, W=16 103.1 -> 97.5; at W=9 and 10 one channel was 2.5 us slower. The
+// forward alone with one channel: 0.3-0.7 us faster at widths 9-12, as much slower at 13-16,
+// hence 2 channels up to 16.
+constexpr int kFwdLongW = 17;
+constexpr int kBwdLongW = 11;
+constexpr int kCplLong = 1;
 constexpr int kMaxGenericW = 128;  // LDS rings of the generic backward (x, g, weights, dweight
                                    // sums: 4 * W * 64 * 4 bytes + the rows' ids, 128.5 KiB at 128);
                                    // wider backwards keep g in the workspace (bwd_g/bwd_wide)
@@ -93,24 +105,37 @@ inline hipError_t launch(const void* kernel, dim3 grid, dim3 block, size_t shmem
   return launch_args(kernel, grid, block, shmem, s, args);
 }
 
-// The vectorised kernels of widths below kFwdWideW and of widths kFwdWideW..kMaxFastW are
-// instantiated in translation units of their own (ccv1d_{fwd,bwd}_<dtype>.hip and
-// ccv1d_{fwd,bwd}_<dtype>_wide.hip), so the build compiles them in parallel.
+// The vectorised kernels are instantiated in translation units of their own per pass, dtype and
+// width range, so the build compiles them in parallel: widths 2..8 (ccv1d_{fwd,bwd}_<dtype>.hip),
+// 9..16 (_wide.hip), 17..24 (_long1.hip) and 25..32 (_long2.hip). First widths of the last three:
+constexpr int kUnitWideW = 9, kUnitLong1W = 17, kUnitLong2W = 25;
 template <typename TX>
 hipError_t launch_fwd_fast_narrow_t(const FwdParams& p, hipStream_t s);
 template <typename TX>
 hipError_t launch_fwd_fast_wide_t(const FwdParams& p, hipStream_t s);
 template <typename TX>
+hipError_t launch_fwd_fast_long1_t(const FwdParams& p, hipStream_t s);
+template <typename TX>
+hipError_t launch_fwd_fast_long2_t(const FwdParams& p, hipStream_t s);
+template <typename TX>
 hipError_t launch_bwd_fast_narrow_t(const BwdParams& p, hipStream_t s);
 template <typename TX>
 hipError_t launch_bwd_fast_wide_t(const BwdParams& p, hipStream_t s);
 template <typename TX>
+hipError_t launch_bwd_fast_long1_t(const BwdParams& p, hipStream_t s);
+template <typename TX>
+hipError_t launch_bwd_fast_long2_t(const BwdParams& p, hipStream_t s);
+template <typename TX>
 inline hipError_t launch_fwd_fast_t(const FwdParams& p, hipStream_t s) {
-  return p.W < kFwdWideW ? launch_fwd_fast_narrow_t<TX>(p, s) : launch_fwd_fast_wide_t<TX>(p, s);
+  if (p.W < kUnitWideW) return launch_fwd_fast_narrow_t<TX>(p, s);
+  if (p.W < kUnitLong1W) return launch_fwd_fast_wide_t<TX>(p, s);
+  return p.W < kUnitLong2W ? launch_fwd_fast_long1_t<TX>(p, s) : launch_fwd_fast_long2_t<TX>(p, s);
 }
 template <typename TX>
 inline hipError_t launch_bwd_fast_t(const BwdParams& p, hipStream_t s) {
-  return p.W < kFwdWideW ? launch_bwd_fast_narrow_t<TX>(p, s) : launch_bwd_fast_wide_t<TX>(p, s);
+  if (p.W < kUnitWideW) return launch_bwd_fast_narrow_t<TX>(p, s);
+  if (p.W < kUnitLong1W) return launch_bwd_fast_wide_t<TX>(p, s);
+  return p.W < kUnitLong2W ? launch_bwd_fast_long1_t<TX>(p, s) : launch_bwd_fast_long2_t<TX>(p, s);
 }
 template <typename TX>
 hipError_t launch_fwd_generic_t(const FwdParams& p, hipStream_t s);
@@ -148,13 +173,17 @@ static hipError_t fwd_one(const FwdParams& p, hipStream_t s) {
 }
 
 // The channels per lane the host's tiling chose (Tiling::vec): CPL or CPL_SMALL below kFwdWideW,
-// CPL_SMALL from it. Any other value is rejected.
+// CPL_SMALL from it, kCplLong from kFwdLongW. Any other value is rejected.
 template <typename TX, int W, bool SILU, bool SEQ>
 static hipError_t fwd_vec(const FwdParams& p, hipStream_t s) {
   using C = FwdCfg<TX>;
-  if (p.tl.vec == C::CPL_SMALL) return fwd_one<TX, W, SILU, SEQ, C::CPL_SMALL>(p, s);
-  if constexpr (W < kFwdWideW) {
-    if (p.tl.vec == C::CPL) return fwd_one<TX, W, SILU, SEQ, C::CPL>(p, s);
+  if constexpr (W >= kFwdLongW) {
+    if (p.tl.vec == kCplLong) return fwd_one<TX, W, SILU, SEQ, kCplLong>(p, s);
+  } else {
+    if (p.tl.vec == C::CPL_SMALL) return fwd_one<TX, W, SILU, SEQ, C::CPL_SMALL>(p, s);
+    if constexpr (W < kFwdWideW) {
+      if (p.tl.vec == C::CPL) return fwd_one<TX, W, SILU, SEQ, C::CPL>(p, s);
+    }
   }
   return hipErrorInvalidValue;
 }
@@ -184,13 +213,17 @@ static hipError_t bwd_one(const BwdParams& p, hipStream_t s) {
 }
 
 // The channels per lane the host's tiling chose (Tiling::vec): CPL_WIDE from kBwdWideW up; below
-// it CPL or CPL_WIDE. Any other value is rejected.
+// it CPL or CPL_WIDE; kCplLong from kBwdLongW. Any other value is rejected.
 template <typename TX, int W, bool SILU, bool SEQ>
 static hipError_t bwd_vec(const BwdParams& p, hipStream_t s) {
   using C = BwdCfg<TX>;
-  if (p.tl.vec == C::CPL_WIDE) return bwd_one<TX, W, SILU, SEQ, C::CPL_WIDE>(p, s);
-  if constexpr (W < kBwdWideW) {
-    if (p.tl.vec == C::CPL) return bwd_one<TX, W, SILU, SEQ, C::CPL>(p, s);
+  if constexpr (W >= kBwdLongW) {
+    if (p.tl.vec == kCplLong) return bwd_one<TX, W, SILU, SEQ, kCplLong>(p, s);
+  } else {
+    if (p.tl.vec == C::CPL_WIDE) return bwd_one<TX, W, SILU, SEQ, C::CPL_WIDE>(p, s);
+    if constexpr (W < kBwdWideW) {
+      if (p.tl.vec == C::CPL) return bwd_one<TX, W, SILU, SEQ, C::CPL>(p, s);
+    }
   }
   return hipErrorInvalidValue;
 }
@@ -263,6 +296,66 @@ hipError_t launch_bwd_fast_wide_t(const BwdParams& p, hipStream_t s) {
     case 14: return bwd_w<TX, 14>(p, s);
     case 15: return bwd_w<TX, 15>(p, s);
     case 16: return bwd_w<TX, 16>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename TX>
+hipError_t launch_fwd_fast_long1_t(const FwdParams& p, hipStream_t s) {
+  switch (p.W) {
+    case 17: return fwd_w<TX, 17>(p, s);
+    case 18: return fwd_w<TX, 18>(p, s);
+    case 19: return fwd_w<TX, 19>(p, s);
+    case 20: return fwd_w<TX, 20>(p, s);
+    case 21: return fwd_w<TX, 21>(p, s);
+    case 22: return fwd_w<TX, 22>(p, s);
+    case 23: return fwd_w<TX, 23>(p, s);
+    case 24: return fwd_w<TX, 24>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename TX>
+hipError_t launch_fwd_fast_long2_t(const FwdParams& p, hipStream_t s) {
+  switch (p.W) {
+    case 25: return fwd_w<TX, 25>(p, s);
+    case 26: return fwd_w<TX, 26>(p, s);
+    case 27: return fwd_w<TX, 27>(p, s);
+    case 28: return fwd_w<TX, 28>(p, s);
+    case 29: return fwd_w<TX, 29>(p, s);
+    case 30: return fwd_w<TX, 30>(p, s);
+    case 31: return fwd_w<TX, 31>(p, s);
+    case 32: return fwd_w<TX, 32>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename TX>
+hipError_t launch_bwd_fast_long1_t(const BwdParams& p, hipStream_t s) {
+  switch (p.W) {
+    case 17: return bwd_w<TX, 17>(p, s);
+    case 18: return bwd_w<TX, 18>(p, s);
+    case 19: return bwd_w<TX, 19>(p, s);
+    case 20: return bwd_w<TX, 20>(p, s);
+    case 21: return bwd_w<TX, 21>(p, s);
+    case 22: return bwd_w<TX, 22>(p, s);
+    case 23: return bwd_w<TX, 23>(p, s);
+    case 24: return bwd_w<TX, 24>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename TX>
+hipError_t launch_bwd_fast_long2_t(const BwdParams& p, hipStream_t s) {
+  switch (p.W) {
+    case 25: return bwd_w<TX, 25>(p, s);
+    case 26: return bwd_w<TX, 26>(p, s);
+    case 27: return bwd_w<TX, 27>(p, s);
+    case 28: return bwd_w<TX, 28>(p, s);
+    case 29: return bwd_w<TX, 29>(p, s);
+    case 30: return bwd_w<TX, 30>(p, s);
+    case 31: return bwd_w<TX, 31>(p, s);
+    case 32: return bwd_w<TX, 32>(p, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -5,7 +5,9 @@ Tolerances (from the build's north star):
   * bf16/fp16 out, dx, dinit: |gpu - ref| <= 1e-2 + 1e-2 |ref|, ref = the oracle's fp32 value. The
     kernels evaluate every output in the oracle's operation order, so without an activation the
     results are also required to be bit-identical to the oracle rounded to the output dtype, and
-    with silu at least 99% of them must be (the exp/reciprocal implementations differ by ulps).
+    with silu all but 1% of them, plus one, must be (the exp/reciprocal implementations and the
+    place of the bias in the sum differ by fp32 ulps, which flips about 1e-4 of the roundings; the
+    one extra value keeps a sample of a few values from failing on a single flip).
   * fp32 out, dx, dinit: |gpu - ref| <= 1e-5 + 1e-5 |ref|.
   * dweight, dbias (fp32): |gpu - ref| <= 1e-3 |ref| + 1e-5 rms(ref), ref summed in double. The
     absolute term covers entries near zero, where the rounding of any fp32 accumulation over the
@@ -132,11 +134,12 @@ def check_lowp(gpu, ref32, exact, what):
         return
     torch.testing.assert_close(gpu.float(), ref, rtol=1e-2, atol=1e-2, msg=what)
     same = (gpu == ref.to(gpu.dtype)) | (gpu.isnan() & ref.to(gpu.dtype).isnan())
-    frac = same.float().mean().item() if same.numel() else 1.0
+    differ = same.numel() - int(same.sum())
     if exact:
-        assert frac == 1.0, f"{what}: {1 - frac:.2e} of values differ from the oracle's rounding"
+        assert differ == 0, f"{what}: {differ} of {same.numel()} values differ from the oracle's rounding"
     else:
-        assert frac >= 0.99, f"{what}: only {frac:.4f} of values match the oracle's rounding"
+        assert differ <= 0.01 * same.numel() + 1, \
+            f"{what}: {differ} of {same.numel()} values differ from the oracle's rounding"
 
 
 def check_sum(gpu, ref64, what):
@@ -187,11 +190,11 @@ def test_readme_example():
     compare(gpu, oracle_ref(inp, True), True)
 
 
-@pytest.mark.parametrize("W", [2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 15, 16, 17, 24])
+@pytest.mark.parametrize("W", [2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 15, 16, 17, 20, 24, 25, 31, 32])
 @pytest.mark.parametrize("act", [None, "silu"])
 def test_widths_and_lengths(W, act):
-    """Widths of the register-window kernels (2-16) and of the generic ones (17, 24), at lengths
-    around the window (T = P - 1, P, P + 1) and beyond, with state handoff both ways."""
+    """Widths of the register-window kernels (2-32; one channel per lane from 17), at lengths around
+    the window (T = P - 1, P, P + 1) and beyond, with state handoff both ways."""
     P = W - 1
     for T in sorted({1, max(1, P - 1), P, P + 1, 17, 1000}):
         for D in (8, 1024):
@@ -264,7 +267,7 @@ def test_strided_x_and_dout(layout):
     compare(gpu, oracle_ref(inp, True, need_dinit=True), True)
 
 
-@pytest.mark.parametrize("W", [2, 4, 7])
+@pytest.mark.parametrize("W", [2, 4, 7, 20, 32])
 @pytest.mark.parametrize("init", [False, True])
 def test_seq_idx(W, init):
     B, T, D = 3, 2000, 512
@@ -279,7 +282,7 @@ def test_seq_idx(W, init):
     assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0)
 
 
-@pytest.mark.parametrize("W", [4, 7])
+@pytest.mark.parametrize("W", [4, 7, 24])
 def test_seq_idx_long_segments(W):
     """Long segments with few boundaries: most tiles lie inside one segment (and run the seq-free
     code), the others carry a boundary or padding; both kinds must match the oracle, and padding
@@ -293,7 +296,7 @@ def test_seq_idx_long_segments(W):
     assert torch.all(gpu["out"][pad] == 0) and torch.all(gpu["dx"][pad] == 0)
 
 
-@pytest.mark.parametrize("W", [4, 7])
+@pytest.mark.parametrize("W", [4, 7, 32])
 def test_seq_idx_padding_runs(W):
     """Runs of padding long enough to hold whole tiles, which take the padding path (forward: zero
     stores; backward: g = 0, no dout reads): at the start of a row (with initial states, whose rows
@@ -615,13 +618,14 @@ def test_forward_cache_policies_leave_results_unchanged(case):
     check_lowp(_sub(out.cpu(), cols), ref["out"], False, "out")
 
 
-@pytest.mark.parametrize("W", [17, 64, 100, 128])
-@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("W,xdt", [(33, torch.bfloat16), (33, torch.float32), (64, torch.bfloat16),
+                                   (64, torch.float32), (100, torch.bfloat16), (100, torch.float32),
+                                   (128, torch.bfloat16), (128, torch.float32), (20, torch.float64)])
 def test_generic_ring_widths(W, xdt):
-    """Widths 17-128 run the generic kernels with their weights and row windows in LDS; from width
-    64 the backward's LDS exceeds the default 64 KiB and the launcher raises the kernel's limit.
-    Against the oracle around the window length, with initial and final states and their
-    gradients, and with seq_idx."""
+    """Widths 33-128 (and fp64 x from width 2) run the generic kernels with their weights and row
+    windows in LDS; from width 64 the backward's LDS exceeds the default 64 KiB and the launcher
+    raises the kernel's limit. Against the oracle around the window length, with initial and final
+    states and their gradients, and with seq_idx."""
     D = 72
     for T in (1, W - 1, W + 1, 300):
         init = T % 2 == 1
@@ -634,6 +638,33 @@ def test_generic_ring_widths(W, xdt):
     gpu = run_gpu(inp, "silu", init_grad=True)
     compare(gpu, oracle_ref(inp, True, need_dinit=True), True)
     assert torch.all(gpu["out"][seq < 0] == 0) and torch.all(gpu["dx"][seq < 0] == 0)
+
+
+@pytest.mark.parametrize("W", [17, 32])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16, torch.float32])
+def test_long_widths_dtypes_and_offsets(W, xdt):
+    """Widths 17-32 take one channel per lane, so any channel count and any channel offset of x
+    (rows aligned to one element only) run the register-window kernels: dims 72 and 1000, and x,
+    dout a slice at an odd channel offset of a wider tensor; with states and their gradients."""
+    for D, T in ((72, 300), (1000, 700)):
+        inp = make_inputs(11 * W + D, 2, T, D, W, xdt=xdt, init=True)
+        gpu = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=True)
+        compare(gpu, oracle_ref(inp, True, final=True, dfinal=True, need_dinit=True), True)
+    B, T, D, off = 2, 500, 200, 3
+    inp = make_inputs(13 * W, B, T, D, W, xdt=xdt, init=True)
+    big = torch.zeros(B, T, D + 9, dtype=xdt)
+    big[..., off:off + D] = inp["x"]
+    x = big.to(DEV)[..., off:off + D].detach().requires_grad_(True)
+    dyb = torch.zeros(B, T, D + 5, dtype=xdt)
+    dyb[..., 1:1 + D] = inp["dy"]
+    w = inp["w"].to(DEV).requires_grad_(True)
+    b = inp["b"].to(DEV).requires_grad_(True)
+    init = inp["init"].to(DEV).requires_grad_(True)
+    out = causal_conv1d_fn(x, w, b, initial_states=init, activation="silu")
+    out.backward(dyb.to(DEV)[..., 1:1 + D])
+    gpu = {"out": out.detach().cpu(), "dx": x.grad.cpu(), "dw": w.grad.cpu(), "db": b.grad.cpu(),
+           "dinit": init.grad.cpu()}
+    compare(gpu, oracle_ref(inp, True, need_dinit=True), True)
 
 
 @pytest.mark.parametrize("W", [129, 200, 257])
