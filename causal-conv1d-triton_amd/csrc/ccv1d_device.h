@@ -75,6 +75,17 @@ struct ReduceParams {
 // Scalar conversions for the side tensors (weight, bias, states) whose dtype is a runtime code.
 // ---------------------------------------------------------------------------------------------
 
+// An fp32 result converted to the type T it is stored in, rounded from its fp32 value as the
+// reference's stores round it. For 16-bit T the value first passes through an empty asm: without
+// it the compiler may fold the conversion into the fma that produced the value (v_fma_mixlo_f16
+// rounds the exact a * b + c to fp16 once), which differs from rounding the fp32 result in about
+// one value in 10^5.
+template <typename T>
+__device__ __forceinline__ T to_store(float v) {
+  if constexpr (sizeof(T) == 2) asm("" : "+v"(v));
+  return static_cast<T>(v);
+}
+
 __device__ __forceinline__ float ld_any(const void* p, int64_t i, int dt) {
   switch (dt) {
     case DT_F32: return static_cast<const float*>(p)[i];
@@ -87,8 +98,8 @@ __device__ __forceinline__ float ld_any(const void* p, int64_t i, int dt) {
 __device__ __forceinline__ void st_any(void* p, int64_t i, int dt, float v) {
   switch (dt) {
     case DT_F32: static_cast<float*>(p)[i] = v; break;
-    case DT_F16: static_cast<_Float16*>(p)[i] = static_cast<_Float16>(v); break;
-    case DT_BF16: static_cast<__bf16*>(p)[i] = static_cast<__bf16>(v); break;
+    case DT_F16: static_cast<_Float16*>(p)[i] = to_store<_Float16>(v); break;
+    case DT_BF16: static_cast<__bf16*>(p)[i] = to_store<__bf16>(v); break;
     default: static_cast<double*>(p)[i] = static_cast<double>(v); break;
   }
 }
@@ -150,7 +161,7 @@ struct VecIO {
   // Round-to-nearest-even; one v_cvt_pk_{bf16,f16}_f32 per channel pair.
   __device__ static __forceinline__ raw pack(const float (&f)[CPL]) {
     if constexpr (BYTES == 2) {
-      return __builtin_bit_cast(raw, static_cast<TX>(f[0]));
+      return __builtin_bit_cast(raw, to_store<TX>(f[0]));
     } else {
       raw v;
 #pragma unroll
@@ -310,12 +321,12 @@ __device__ __forceinline__ void st_vec_any(void* p, int64_t off, int dt, const f
     case DT_F16: {
       _Float16* q = static_cast<_Float16*>(p) + off;
 #pragma unroll
-      for (int i = 0; i < N; ++i) q[i] = static_cast<_Float16>(f[i]);
+      for (int i = 0; i < N; ++i) q[i] = to_store<_Float16>(f[i]);
     } break;
     case DT_BF16: {
       __bf16* q = static_cast<__bf16*>(p) + off;
 #pragma unroll
-      for (int i = 0; i < N; ++i) q[i] = static_cast<__bf16>(f[i]);
+      for (int i = 0; i < N; ++i) q[i] = to_store<__bf16>(f[i]);
     } break;
     default: {
       double* q = static_cast<double*>(p) + off;

@@ -70,11 +70,11 @@ __global__ __launch_bounds__(64) void fwd_generic_kernel(const FwdParams p) {
     if (p.has_bias) z += bias;
     if (sb && st < 0) z = 0.0f;
     if (silu) z = z * sigmoid_f(z);
-    ob[t * D] = static_cast<TX>(z);
+    ob[t * D] = to_store<TX>(z);
   }
   if (p.has_final && t1 == T) {
     TX* fb = static_cast<TX*>(p.fin) + (int64_t)b * P * D + c;
-    for (int q = 0; q < P; ++q) fb[q * D] = static_cast<TX>(xx(T - P + q));
+    for (int q = 0; q < P; ++q) fb[q * D] = to_store<TX>(xx(T - P + q));
   }
 }
 
@@ -152,13 +152,13 @@ __global__ __launch_bounds__(64) void fwd_generic_ring_kernel(const FwdParams p)
       if (p.has_bias) z += bias;
       if (sb && st < 0) z = 0.0f;
       if (p.silu) z = z * sigmoid_f(z);
-      ob[(int64_t)t * D] = static_cast<TX>(z);
+      ob[(int64_t)t * D] = to_store<TX>(z);
       slot = ring_next(slot, W);
     }
   }
   if (p.has_final && t1 == T) {
     TX* fb = static_cast<TX*>(p.fin) + (int64_t)b * P * D + c;
-    for (int q = 0; q < P; ++q) fb[q * D] = static_cast<TX>(xx(T - P + q));
+    for (int q = 0; q < P; ++q) fb[q * D] = to_store<TX>(xx(T - P + q));
   }
 }
 
@@ -229,7 +229,7 @@ __global__ __launch_bounds__(64) void bwd_generic_ring_kernel(const BwdParams p)
       const int f = row - (T - P);
       if (f >= 0 && f < P) dx += static_cast<float>(dfb[f * D]);
     }
-    if (row >= 0) dxb[(int64_t)row * p.s_dxt] = static_cast<TX>(dx);
+    if (row >= 0) dxb[(int64_t)row * p.s_dxt] = to_store<TX>(dx);
     else st_any(dinitb, (int64_t)(row + P) * D, p.i_dt, dx);
   };
 
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(64) void bwd_wide_kernel(const BwdParams p, const f
       const int f = row - (T - P);
       if (f >= 0 && f < P) dx += static_cast<float>(dfb[(int64_t)f * D]);
     }
-    if (row >= 0) dxb[(int64_t)row * p.s_dxt] = static_cast<TX>(dx);
+    if (row >= 0) dxb[(int64_t)row * p.s_dxt] = to_store<TX>(dx);
     else st_any(dinitb, (int64_t)(row + P) * D, p.i_dt, dx);
   }
 

@@ -229,15 +229,20 @@ def test_wide_widths_channel_counts(W, D, xdt):
 def test_dtypes(xdt, wdt):
     """Every x dtype against every weight/bias dtype, with initial states in a third dtype (fp32
     for fp32 weights, the other 16-bit type for 16-bit weights), so the conversions on load and
-    the stores of dweight, dbias and the initial-state gradient in their own dtype all run."""
+    the stores of dweight, dbias and the initial-state gradient in their own dtype all run; widths
+    4 (vectorised kernels and, with a dim that is not a multiple of 4, the generic ones), 12 and 20
+    (one channel per lane). Without the activation out, dx and dinit must be bit-identical to the
+    oracle's fp32 values rounded once to their dtype."""
     idt = {torch.float32: torch.float32, torch.bfloat16: torch.float16,
            torch.float16: torch.bfloat16}[wdt]
-    for D in (256, 250):  # vectorised kernels, and the generic ones (dim not a multiple of 4)
-        inp = make_inputs(7, 2, 257, D, 4, xdt=xdt, wdt=wdt, init=True, idt=idt)
-        gpu = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=True)
-        assert gpu["out"].dtype == xdt and gpu["dx"].dtype == xdt
-        assert gpu["dw"].dtype == wdt and gpu["db"].dtype == wdt and gpu["dinit"].dtype == idt
-        compare(gpu, oracle_ref(inp, True, final=True, dfinal=True, need_dinit=True), True)
+    for W, D in ((4, 256), (4, 250), (12, 250), (20, 250)):
+        for act in ("silu", None):
+            inp = make_inputs(7 + W, 2, 257, D, W, xdt=xdt, wdt=wdt, init=True, idt=idt)
+            gpu = run_gpu(inp, act, return_final=True, dfinal=True, init_grad=True)
+            assert gpu["out"].dtype == xdt and gpu["dx"].dtype == xdt
+            assert gpu["dw"].dtype == wdt and gpu["db"].dtype == wdt and gpu["dinit"].dtype == idt
+            compare(gpu, oracle_ref(inp, act is not None, final=True, dfinal=True, need_dinit=True),
+                    act is not None)
 
 
 @pytest.mark.parametrize("layout", ["time_stride", "aligned_slice", "misaligned_slice"])
@@ -644,12 +649,16 @@ def test_generic_ring_widths(W, xdt):
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16, torch.float32])
 def test_long_widths_dtypes_and_offsets(W, xdt):
     """Widths 17-32 take one channel per lane, so any channel count and any channel offset of x
-    (rows aligned to one element only) run the register-window kernels: dims 72 and 1000, and x,
-    dout a slice at an odd channel offset of a wider tensor; with states and their gradients."""
-    for D, T in ((72, 300), (1000, 700)):
-        inp = make_inputs(11 * W + D, 2, T, D, W, xdt=xdt, init=True)
-        gpu = run_gpu(inp, "silu", return_final=True, dfinal=True, init_grad=True)
-        compare(gpu, oracle_ref(inp, True, final=True, dfinal=True, need_dinit=True), True)
+    (rows aligned to one element only) run the register-window kernels: dims 72 (with a bias) and
+    1000 (without), with and without the activation (without it bit-identical to the oracle:
+    16-bit results rounded once from their fp32 values), and x, dout a slice at an odd
+    channel offset of a wider tensor; with states and their gradients."""
+    for D, T, bias in ((72, 300, True), (1000, 700, False)):
+        for act in ("silu", None):
+            inp = make_inputs(11 * W + D, 2, T, D, W, xdt=xdt, bias=bias, init=True)
+            gpu = run_gpu(inp, act, return_final=True, dfinal=True, init_grad=True)
+            compare(gpu, oracle_ref(inp, act is not None, final=True, dfinal=True, need_dinit=True),
+                    act is not None)
     B, T, D, off = 2, 500, 200, 3
     inp = make_inputs(13 * W, B, T, D, W, xdt=xdt, init=True)
     big = torch.zeros(B, T, D + 9, dtype=xdt)
