@@ -523,7 +523,7 @@ def _random_seq(g, B, T):
     return s
 
 
-@pytest.mark.parametrize("case", range(48))
+@pytest.mark.parametrize("case", range(96))
 def test_random_cases(case):
     """Random shapes, widths, dtypes and options (bias, activation, initial states, seq_idx with
     padding runs, final states with their gradient) against the oracle."""
@@ -532,7 +532,7 @@ def test_random_cases(case):
     B = pick([1, 2, 3, 4])
     T = pick([1, 2, 5, 9, 17, 64, 100, 333, 700])
     D = pick([8, 64, 100, 256, 264, 1000, 1024])
-    W = pick([2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 20])
+    W = pick([2, 3, 4, 5, 6, 7, 8, 9, 11, 12, 13, 16, 17, 20, 24, 25, 32, 33])
     xdt = pick([torch.bfloat16, torch.bfloat16, torch.float16, torch.float32])
     wdt = pick([torch.float32, torch.float32, torch.bfloat16, torch.float16])
     idt = pick([None, torch.float32, torch.bfloat16, torch.float16])
