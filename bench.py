@@ -298,13 +298,15 @@ def _alg_bytes_general(B, T, D, W, bias, init=False, seq=False, final=False, ex=
     return fwd, bwd
 
 
-def run_configs(dev, widths=False, only=None):
+def run_configs(dev, widths=False, only=None, shapes=False):
     """One JSON line per BASELINE configuration 2-5 (the reference's README sweep, the Mamba-2 xBC
     shape, chunked streaming and decode with state handoff, packed varlen seq_idx): device time per
     call from replayed graphs after the usual warm-up, plus, for the latency-bound streaming and
     decode calls, the host-inclusive eager time per call. With `widths`, instead: the benchmark
     shape (bf16, bias + silu) at every width the vectorised kernels cover, forward alone and
-    forward + backward (widths 2-8, 9, 12, 16, 17, 20, 24 and 32).
+    forward + backward (widths 2-8, 9, 12, 16, 17, 20, 24 and 32). With `shapes`, instead: the
+    same two passes over mid-size shapes (many batch rows or short sequences, where the tiling's
+    choice of tile length matters) at widths 4, 6, 8, 9, 12, 16 and 24.
 
     `only` (a set of strings, e.g. {"2:512", "5:7"} or, with `widths`, {"8"}) restricts the run to
     the named configurations (N, or N:T for configuration 2's lengths, N:W for configuration 5's
@@ -372,6 +374,26 @@ def run_configs(dev, widths=False, only=None):
             shape = f"B={B} T={T} D={D} W={W} bias_silu"
             emit("widths", shape, timed(fwds(sets, w, b, "silu"), len(sets)), fb, bb, "fwd")
             emit("widths", shape, timed(steps(sets, w, b, "silu"), len(sets)), fb, bb, "fwd+bwd")
+        return
+
+    if shapes:
+        for B, T, D in ((16, 2048, 2048), (32, 1024, 2048), (8, 1024, 4096), (64, 512, 2048),
+                        (8, 4096, 4096), (2, 8192, 2048)):
+            nsets = max(2, min(4, (512 << 20) // (B * T * D * 2)))
+            sets = [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
+                     .requires_grad_(True),
+                     torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
+                    for _ in range(nsets)]
+            b = torch.randn(D, generator=gen, device=dev).requires_grad_(True)
+            for W in (4, 6, 8, 9, 12, 16, 24):
+                if only and str(W) not in only:
+                    continue
+                w = (torch.randn(D, W, generator=gen, device=dev) / math.sqrt(W)).requires_grad_(True)
+                fb, bb = _alg_bytes_general(B, T, D, W, True)
+                shape = f"B={B} T={T} D={D} W={W} bias_silu"
+                emit("shapes", shape, timed(fwds(sets, w, b, "silu"), nsets), fb, bb, "fwd")
+                emit("shapes", shape, timed(steps(sets, w, b, "silu"), nsets), fb, bb, "fwd+bwd")
+            del sets
         return
 
     # Configuration 2: README shape sweep, B=4 D=1024 W=4, weight only or bias + silu.
@@ -543,9 +565,11 @@ def main():
                     help="instead of the headline line, one JSON line per BASELINE configuration 2-5")
     ap.add_argument("--widths", action="store_true",
                     help="instead of the headline line, the benchmark shape at widths 2-32")
+    ap.add_argument("--shapes", action="store_true",
+                    help="instead of the headline line, mid-size shapes at widths 4-24")
     ap.add_argument("--only", default="",
-                    help="with --configs or --widths: comma-separated workloads to run (e.g. "
-                         "2:512,5:7 or, with --widths, 8)")
+                    help="with --configs, --widths or --shapes: comma-separated workloads to run "
+                         "(e.g. 2:512,5:7 or, with --widths or --shapes, widths such as 8)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -560,8 +584,8 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    if args.configs or args.widths:
-        run_configs(dev, widths=args.widths,
+    if args.configs or args.widths or args.shapes:
+        run_configs(dev, widths=args.widths, shapes=args.shapes,
                     only={t for t in args.only.split(",") if t} or None)
         return
     B, T, D, W = 4, 8192, 1024, 4

@@ -141,18 +141,32 @@ bool fwd_out_streams(bool inference, int64_t B, int64_t T, int64_t D, int x_dt) 
 // to the shortest tile). With fewer, every dispatch wave of the grid covers few rows of many
 // columns: measured at B=8 T=4096 D=4096 (8 workgroups per column with 64-row tiles) the step took
 // 293 us against 243 us with 32-row tiles; at B=4 T=8192 D=4096 (16 per column) 64 rows stay
-// better (248 vs 251 us).
+// better (248 vs 251 us). That holds for the backward with 4 channels per lane and the forward below
+// kFwdLongTileW. The backward with 2 or 1 channels per lane (widths from 6, and small grids) and the
+// forward from kFwdLongTileW (its window of W - 1 halo rows is re-read per tile) take the longest
+// tile the wave target allows, however few workgroups that leaves along time (the rule is not
+// applied). Measured on one box, bf16, bias + silu, the rule's tiles against 64-row tiles:
+//   fwd+bwd step: B=8 T=4096 D=4096 W=6 251 -> 238 us, W=9 292 -> 270, W=16 426 -> 382, W=24 701
+//   -> 580; B=8 T=4096 D=5376 W=7 357 -> 335, W=20 775 -> 653; B=32 T=1024 D=2048 W=6 145 -> 137,
+//   W=16 226 -> 201; B=8 T=1024 D=4096 W=8 94 -> 78; B=64 T=512 D=2048 W=12 184 -> 166; (W=4, 4
+//   channels: B=8 T=4096 D=4096 227 against 243 with 64 rows, the benchmark shape 60.4 against
+//   62.5);
+//   forward alone: B=8 T=4096 D=4096 W=12 113 -> 104 us, W=16 131 -> 112, W=24 169 -> 151;
+//   B=16 T=2048 D=2048 W=16 83 -> 62; B=64 T=512 D=2048 W=16 83 -> 59 (W=4-9 mixed: B=8 T=4096
+//   D=4096 W=4 99 against 133 with 64 rows, W=9 108 against 113).
 constexpr int64_t kMinTimeWorkgroups = 16;
+constexpr int kFwdLongTileW = 12;
 
 // Waves the vectorised kernels' tilings aim for (16 per CU).
 constexpr int64_t kTargetWaves = 4096;
 
 // Tiling of the vectorised kernels: the longest tile (fewest halo re-reads) that still gives the
-// grid `target_waves` waves and every column kMinTimeWorkgroups workgroups along time, a function
+// grid `target_waves` waves and every column `min_time_wg` workgroups along time, a function
 // of the shape alone so that results, including the dweight summation order, do not depend on the
 // device.
 Tiling fast_tiling(int64_t B, int64_t T, int64_t D, int vec, int nw, int lmin, int lmax,
-                   int64_t target_waves, int override_rows) {
+                   int64_t target_waves, int override_rows,
+                   int64_t min_time_wg = kMinTimeWorkgroups) {
   Tiling t{};
   const int64_t G = D / vec;
   t.nGW = (int32_t)cdiv(G, 64);
@@ -161,7 +175,7 @@ Tiling fast_tiling(int64_t B, int64_t T, int64_t D, int vec, int nw, int lmin, i
     L = override_rows;
   } else {
     while (L > lmin && (B * cdiv(T, L) * t.nGW < target_waves ||
-                        cdiv(cdiv(T, L), nw) < kMinTimeWorkgroups))
+                        cdiv(cdiv(T, L), nw) < min_time_wg))
       L >>= 1;
   }
   t.L = L;
@@ -180,7 +194,9 @@ constexpr int64_t kFwdSmallGrid = 256;
 Tiling fwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw) {
   const int lmin = min_tile_rows(W);
   const int over = tune().fwd_rows >= lmin ? tune().fwd_rows : 0;
-  Tiling t = fast_tiling(B, T, D, cpl, nw, lmin > 16 ? lmin : 16, kMaxTileRows, kTargetWaves, over);
+  const int64_t min_time_wg = W >= kFwdLongTileW ? 1 : kMinTimeWorkgroups;
+  Tiling t = fast_tiling(B, T, D, cpl, nw, lmin > 16 ? lmin : 16, kMaxTileRows, kTargetWaves, over,
+                         min_time_wg);
   if (over == 0 && t.L == 16 && lmin < 16 && t.nBlk < kFwdSmallGrid)
     t = fast_tiling(B, T, D, cpl, nw, lmin, lmin, kTargetWaves, lmin);
   return t;
@@ -231,7 +247,8 @@ constexpr int64_t kBwdSmallGrid = 256;
 Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw) {
   const int lmin = min_tile_rows(W);
   const int over = tune().bwd_rows >= lmin ? tune().bwd_rows : 0;
-  Tiling t = fast_tiling(B, T, D, cpl, nw, 32, kMaxTileRows, kTargetWaves, over);
+  const int64_t min_time_wg = cpl >= 4 ? kMinTimeWorkgroups : 1;
+  Tiling t = fast_tiling(B, T, D, cpl, nw, 32, kMaxTileRows, kTargetWaves, over, min_time_wg);
   while (over == 0 && t.nBlk < kBwdSmallGrid && t.L > lmin)
     t = fast_tiling(B, T, D, cpl, nw, t.L / 2, t.L / 2, kTargetWaves, t.L / 2);
   return t;

@@ -253,7 +253,7 @@ __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBu
 
   FwdLane<TX, W, SILU, SEQ, CPL> s;
   load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
-  // Every tile is at least min_tile_rows(W) > P rows long (the host's tiling; static_assert in
+  // Every tile is at least min_tile_rows(W) > P rows long (the host's tiling, min_tile_rows in
   // ccv1d_api.hip), so a tile starts at row 0 or at a row >= P: a window not in x is the first
   // tile's, the P initial-state rows (or zeros).
   if (halo_in_x) {
@@ -658,7 +658,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
         s.bv[i] *= kNegLog2e;
       }
     }
-    // Every tile is at least min_tile_rows(W) > P rows long (the host's tiling; static_assert in
+    // Every tile is at least min_tile_rows(W) > P rows long (the host's tiling, min_tile_rows in
     // ccv1d_api.hip), so a tile starts at row 0 or at a row >= P: a window not in x is the first
     // tile's, the P initial-state rows (or zeros).
     if (halo_in_x) {
