@@ -378,7 +378,9 @@ def run_configs(dev, widths=False, only=None, shapes=False):
 
     if shapes:
         for B, T, D in ((16, 2048, 2048), (32, 1024, 2048), (8, 1024, 4096), (64, 512, 2048),
-                        (8, 4096, 4096), (2, 8192, 2048)):
+                        (8, 4096, 4096), (2, 8192, 2048), (16, 512, 4096), (48, 1024, 1024),
+                        (24, 1024, 3072), (4, 1024, 8192), (12, 2048, 2560), (6, 2048, 4096),
+                        (8, 4096, 3072)):
             nsets = max(2, min(4, (512 << 20) // (B * T * D * 2)))
             sets = [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
                      .requires_grad_(True),
