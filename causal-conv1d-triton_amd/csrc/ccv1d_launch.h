@@ -194,10 +194,14 @@ static hipError_t fwd_vec(const FwdParams& p, hipStream_t s) {
 // 5-8) except with seq_idx from width 5, whose kernel also holds the sequence ids. Measured (fwd+bwd
 // step, bf16, R = 4 against 2): B=4 T=8192 D=1024 W=6 -1.2 %, W=7 -2.8 %, W=8 -2.5 %; B=8 T=4096
 // D=5376 W=8 -0.4 %; with seq_idx (B=4 T=16384 D=4096 W=7) +1 %, hence 2 there. Width 5 with 4
-// channels and 4 rows spills.
+// channels and 4 rows spills. With one channel per lane, width 20 takes 2 rows: 128 VGPRs, 4 waves
+// per SIMD, against 134 and 3 waves with 4 rows (step B=4 T=8192 D=1024 133.5 -> 117.1 us, B=8
+// T=4096 D=4096 489 -> 438); at the other widths from 17, 2 rows were 0-6 % slower (no change of
+// occupancy, or none that paid: W=21 137.5 -> 144, W=24 147 -> 154).
 template <typename TX, int W, bool SEQ, int CPL>
 constexpr int bwd_rows() {
   using C = BwdCfg<TX>;
+  if (CPL == 1 && W == 20) return 2;
   if (W <= 4 && CPL * (int)sizeof(TX) <= 8) return C::R;
   if (!SEQ && CPL * (int)sizeof(TX) <= 4) return C::R;
   return 2;
