@@ -715,6 +715,27 @@ def _cols(D, n, seed):
     return torch.cat([idx, torch.tensor([0, D - 1])]).unique()
 
 
+@pytest.mark.parametrize("B,T,D,W,xdt,seq", [
+    (16, 512, 4096, 6, torch.bfloat16, False),   # one workgroup per column along time (64 rows)
+    (32, 1024, 2048, 12, torch.bfloat16, True),  # one channel per lane, seq_idx tiles of all kinds
+    (24, 1024, 3072, 16, torch.float16, False),
+    (6, 2048, 4096, 20, torch.bfloat16, False),  # width 20: 2-row batches
+    (8, 1024, 4096, 24, torch.float32, True),
+    (4, 1024, 8192, 32, torch.bfloat16, False),
+])
+def test_mid_size_long_tiles(B, T, D, W, xdt, seq):
+    """Shapes where the backward (2 or 1 channels per lane) and the forward from width 12 take
+    64-row tiles however few workgroups that leaves along time: a channel subset against the
+    oracle, with initial states and their gradient."""
+    s = varlen_seq(B + W, B, T, lo=64, hi=1024, pad_frac=0.05) if seq else None
+    inp = make_inputs(B * 100 + W, B, T, D, W, xdt=xdt, init=True, seq=s)
+    gpu = run_gpu(inp, "silu", init_grad=True)
+    cols = _cols(D, 24, W)
+    compare(gpu, oracle_ref(inp, True, cols=cols, need_dinit=True), True, cols=cols)
+    if seq:
+        assert torch.all(gpu["out"][s < 0] == 0) and torch.all(gpu["dx"][s < 0] == 0)
+
+
 @pytest.mark.parametrize("T", [512, 2048, 8192, 32768])
 @pytest.mark.parametrize("variant", ["weight_only", "bias_silu"])
 def test_config2_readme_sweep(T, variant):
