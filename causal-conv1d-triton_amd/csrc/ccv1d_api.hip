@@ -161,9 +161,11 @@ constexpr int kFwdLongTileW = 12;
 constexpr int64_t kTargetWaves = 4096;
 
 // Tiling of the vectorised kernels: the longest tile (fewest halo re-reads) that still gives the
-// grid `target_waves` waves and every column `min_time_wg` workgroups along time, a function
-// of the shape alone so that results, including the dweight summation order, do not depend on the
-// device.
+// grid `target_waves` waves, every column `min_time_wg` workgroups along time and at least `nw`
+// tiles along time (a workgroup's waves take consecutive tiles, so fewer would leave some of its
+// waves without one: B=64 T=512 D=2048 W=24 fwd+bwd 283 us with 64-row tiles, 329 with 128, whose
+// 4 tiles fill half of each workgroup), a function of the shape alone so that results, including
+// the dweight summation order, do not depend on the device.
 Tiling fast_tiling(int64_t B, int64_t T, int64_t D, int vec, int nw, int lmin, int lmax,
                    int64_t target_waves, int override_rows,
                    int64_t min_time_wg = kMinTimeWorkgroups) {
@@ -175,7 +177,7 @@ Tiling fast_tiling(int64_t B, int64_t T, int64_t D, int vec, int nw, int lmin, i
     L = override_rows;
   } else {
     while (L > lmin && (B * cdiv(T, L) * t.nGW < target_waves ||
-                        cdiv(cdiv(T, L), nw) < min_time_wg))
+                        cdiv(cdiv(T, L), nw) < min_time_wg || cdiv(T, L) < nw))
       L >>= 1;
   }
   t.L = L;
@@ -244,11 +246,21 @@ Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
 // shape (512 workgroups) keeps 32 rows.
 constexpr int64_t kBwdSmallGrid = 256;
 
-Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw) {
+// Longest tile of the backward with one channel per lane (kCplLong) and no seq_idx: halving the
+// tiles' count halves the work each tile spends outside the pipelined loop (its halo rows, the g
+// rows handed between waves, the partial dweight row), which grows with the width. Measured
+// (fwd+bwd step, bf16, B=4 T=8192 D=1024, 64 against 128 rows in the backward): W=12 83.1 -> 80.7
+// us, W=16 97.9 -> 93.4, W=20 117.1 -> 114.1, W=24 149.6 -> 133.3, W=32 190.5 -> 166.5 (the
+// forward gained nothing from 128-row tiles). With seq_idx a tile and both halos must fit one
+// RowIds, which keeps kMaxTileRows.
+constexpr int kMaxTileRowsLong = 128;
+
+Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw, bool seq) {
   const int lmin = min_tile_rows(W);
   const int over = tune().bwd_rows >= lmin ? tune().bwd_rows : 0;
   const int64_t min_time_wg = cpl >= 4 ? kMinTimeWorkgroups : 1;
-  Tiling t = fast_tiling(B, T, D, cpl, nw, 32, kMaxTileRows, kTargetWaves, over, min_time_wg);
+  const int lmax = cpl == kCplLong && !seq ? kMaxTileRowsLong : kMaxTileRows;
+  Tiling t = fast_tiling(B, T, D, cpl, nw, 32, lmax, kTargetWaves, over, min_time_wg);
   while (over == 0 && t.nBlk < kBwdSmallGrid && t.L > lmin)
     t = fast_tiling(B, T, D, cpl, nw, t.L / 2, t.L / 2, kTargetWaves, t.L / 2);
   return t;
@@ -283,16 +295,16 @@ FastShape bwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
   } else if (W >= kBwdWideW) {
     sh.cpl = cpl_wide(x_dt);
   } else if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
-    const Tiling t = bwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);
+    const Tiling t = bwd_tiling_for(B, T, D, W, sh.cpl, sh.nw, false);
     if (D % sh.cpl || t.L < kBwdNarrowMinRows || B * t.nT * t.nGW < kTargetWaves)
       sh.cpl = cpl_wide(x_dt);
   }
   return sh;
 }
 
-Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
+Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt, bool seq) {
   const FastShape sh = bwd_shape(x_dt, B, T, D, W);
-  return bwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);
+  return bwd_tiling_for(B, T, D, W, sh.cpl, sh.nw, seq);
 }
 
 // Workspace of the backward: the fp32 partial rows of dweight/dbias, (rows, W + 1, D) floats, and
@@ -539,7 +551,8 @@ size_t ccv1d_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t dim, int
   if (B <= 0 || T <= 0 || D <= 0 || W < 2 || !valid_dt(x_dtype)) return 0;
   int64_t rows = B * generic_tiling(T).nT;
   if (W <= kMaxFastW && x_dtype != CCV1D_F64) {
-    const int64_t fr = B * bwd_fast_tiling(B, T, D, W, x_dtype).nTB;
+    // With seq_idx the tiles are never longer, so its tiling has at least as many partial rows.
+    const int64_t fr = B * bwd_fast_tiling(B, T, D, W, x_dtype, true).nTB;
     if (fr > rows) rows = fr;
   }
   size_t n = partial_bytes(rows, W, D);
@@ -690,7 +703,7 @@ int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
             (!dfinal_states || aligned_to(dfinal_states, bcpl * esize(x_dtype))) && ws_aligned;
   int64_t rows;
   if (pl.fast) {
-    p.tl = bwd_fast_tiling(B, T, D, W, x_dtype);
+    p.tl = bwd_fast_tiling(B, T, D, W, x_dtype, seq_idx != nullptr);
     rows = B * p.tl.nTB;
     p.x_bytes = slab_bytes(x_dtype, T, D, x_stride_t);
     p.y_bytes = slab_bytes(x_dtype, T, D, dout_stride_t);
