@@ -725,8 +725,9 @@ def _cols(D, n, seed):
 ])
 def test_mid_size_long_tiles(B, T, D, W, xdt, seq):
     """Shapes where the backward (2 or 1 channels per lane) and the forward from width 12 take
-    64-row tiles however few workgroups that leaves along time: a channel subset against the
-    oracle, with initial states and their gradient."""
+    64-row tiles however few workgroups that leaves along time, and where the backward with one
+    channel per lane and no seq_idx takes 128-row tiles (widths 16, 20 and 32 here): a channel
+    subset against the oracle, with initial states and their gradient."""
     s = varlen_seq(B + W, B, T, lo=64, hi=1024, pad_frac=0.05) if seq else None
     inp = make_inputs(B * 100 + W, B, T, D, W, xdt=xdt, init=True, seq=s)
     gpu = run_gpu(inp, "silu", init_grad=True)
