@@ -65,6 +65,12 @@ def _fwd(x, weight, bias, seq_idx, initial_states, final_states, silu, inference
     """Allocates `out` and runs the forward kernel (reference `_fwd`, causal_conv1d.py:433-472).
     T == 0 is handled inside the library (final_states = initial_states or zeros). `inference`:
     no backward follows (the library then streams out past the caches)."""
+    if not inference and _ffi._torch_native is not None:
+        # Allocation and launch in one native call (None for tensor subclasses).
+        out = _ffi._torch_native.fwd_train(x, weight, bias, seq_idx, initial_states, final_states,
+                                           silu)
+        if out is not None:
+            return out
     B, T, D = x.shape
     out = torch.empty(B, T, D, device=x.device, dtype=x.dtype)
     _ffi.fwd(x, weight, bias, seq_idx, initial_states, out, final_states, silu, inference)
@@ -75,6 +81,12 @@ def _bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, need_din
     """Allocates the gradients and the fp32 partial-sum workspace and runs the backward kernels
     (reference `_bwd`, causal_conv1d.py:475-541). dweight and dbias are always computed; the
     empty-input cases (dweight = dbias = 0, dinit = dfinal) are handled inside the library."""
+    if _ffi._torch_native is not None:
+        # The same checks, allocations and launch in one native call (None for tensor subclasses).
+        res = _ffi._torch_native.bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states,
+                                     need_dinit, silu)
+        if res is not None:
+            return res
     _check_grads(x, dout, dfinal_states)
     B, T, D = x.shape
     W = weight.shape[1]

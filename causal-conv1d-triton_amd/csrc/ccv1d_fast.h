@@ -543,8 +543,10 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Waves per SIMD the backward's register budget is sized for: 4 (128 VGPRs) for the narrow
-// instances, 2 (256 VGPRs) for widths 6..8 and for 16-byte rows at width 5.
+// Waves per SIMD the backward's register budget is sized for: 4 (at most 128 VGPRs) up to width 4
+// and at width 5 with rows of at most 8 bytes (there the fp16 instance with seq_idx spills 16
+// bytes per lane); otherwise 2 (at most 256), within which the instances' own allocation sets the
+// occupancy (4-6 waves at widths 11-20 with one channel per lane, 2-3 from 21).
 template <typename TX, int W, int CPL>
 constexpr int bwd_waves_per_simd() {
   return (W <= 4 || (W == 5 && CPL * (int)sizeof(TX) <= 8)) ? 4 : 2;

@@ -2,7 +2,10 @@
  * in one native call. It takes torch tensors, applies the reference's argument checks and
  * canonicalisation (causal_conv1d.py:397-412, :612-617), allocates the outputs with the caching
  * allocator and calls ccv1d_fwd_inference (include/ccv1d.h: ccv1d_fwd's kernels with the store
- * policy of a pass no backward follows) on torch's current stream of x's device.
+ * policy of a pass no backward follows) on torch's current stream of x's device. For the autograd
+ * node's two passes it also offers `fwd_train` (allocation of out and ccv1d_fwd, on inputs the
+ * Python side has checked and canonicalised) and `bwd` (allocation of the gradients and the
+ * workspace and ccv1d_bwd, the reference's `_bwd`, causal_conv1d.py:475-541).
  *
  * Why native: an eager decode step (batch 16, one row, state handoff) spends about 2.7 us in the
  * HIP launch and, in Python, 1.4 us reading tensor attributes, 2.6 us in two torch.empty calls and
@@ -165,6 +168,141 @@ PyObject* native_fwd(PyObject*, PyObject* const* a, Py_ssize_t n) {
   }
 }
 
+PyObject* library_error(int rc) {
+  PyErr_Format(g_error_type ? g_error_type : PyExc_RuntimeError, "libccv1d error %d: %s", rc,
+               ccv1d_last_error());
+  return nullptr;
+}
+
+// Wraps a tensor, or None for an undefined one; steals nothing on failure.
+PyObject* wrap_or_none(at::Tensor&& t) {
+  if (!t.defined()) Py_RETURN_NONE;
+  return THPVariable_Wrap(std::move(t));
+}
+
+/* fwd_train(x, weight, bias, seq_idx, initial_states, final_states, silu) -> out
+ * The training forward (ccv1d_fwd) on tensors the Python side has checked and canonicalised
+ * (causal_conv1d_fn), writing final_states when given. None when an argument is not a plain
+ * tensor, for the Python path. */
+PyObject* fwd_train_impl(PyObject* const* a) {
+  const at::Tensor *px, *pw, *pb, *ps, *pi, *pf;
+  if (!tensor_or_none(a[0], &px) || !tensor_or_none(a[1], &pw) || !tensor_or_none(a[2], &pb) ||
+      !tensor_or_none(a[3], &ps) || !tensor_or_none(a[4], &pi) || !tensor_or_none(a[5], &pf) ||
+      !px || !pw)
+    Py_RETURN_NONE;
+  const int silu = PyObject_IsTrue(a[6]);
+  if (silu < 0) return nullptr;
+  const at::Tensor& x = *px;
+  const at::Tensor& w = *pw;
+  const int64_t B = x.size(0), T = x.size(1), D = x.size(2), W = w.size(1);
+  const int xdt = dtype_code(x.scalar_type()), wdt = dtype_code(w.scalar_type());
+  const int bdt = pb ? dtype_code(pb->scalar_type()) : 0;
+  const int idt = pi ? dtype_code(pi->scalar_type()) : 0;
+  if (xdt < 0 || wdt < 0 || bdt < 0 || idt < 0) {
+    PyErr_SetString(PyExc_TypeError, "unsupported dtype (fp32, fp16, bf16 or fp64 expected)");
+    return nullptr;
+  }
+  const int64_t dev = x.get_device();
+  at::Tensor out = at::empty({B, T, D}, x.options());
+  void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev)).stream();
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = ccv1d_fwd(x.data_ptr(), x.stride(0), x.stride(1), xdt, w.data_ptr(), wdt,
+                 pb ? pb->data_ptr() : nullptr, bdt,
+                 ps ? static_cast<const int32_t*>(ps->data_ptr()) : nullptr,
+                 pi ? pi->data_ptr() : nullptr, idt, out.data_ptr(),
+                 pf ? pf->data_ptr() : nullptr, B, T, D, W, silu, (int)dev, stream);
+  Py_END_ALLOW_THREADS
+  if (rc) return library_error(rc);
+  return THPVariable_Wrap(std::move(out));
+}
+
+/* bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, need_dinit, silu)
+ *   -> (dx, dweight, dbias or None, dinitial_states or None)
+ * The autograd node's backward (the reference's _bwd, causal_conv1d.py:475-541): x, weight, bias,
+ * seq_idx and initial_states as the forward saved them (checked and canonicalised), dout with a
+ * unit channel stride, dfinal_states contiguous. Allocates the gradients and the fp32 partial-sum
+ * workspace (ccv1d_bwd_workspace_bytes) and calls ccv1d_bwd. None when an argument is not a plain
+ * tensor, for the Python path. */
+PyObject* bwd_impl(PyObject* const* a) {
+  const at::Tensor *px, *pw, *pb, *ps, *pi, *pd, *pf;
+  if (!tensor_or_none(a[0], &px) || !tensor_or_none(a[1], &pw) || !tensor_or_none(a[2], &pb) ||
+      !tensor_or_none(a[3], &ps) || !tensor_or_none(a[4], &pi) || !tensor_or_none(a[5], &pd) ||
+      !tensor_or_none(a[6], &pf) || !px || !pw || !pd)
+    Py_RETURN_NONE;
+  const int need_dinit = PyObject_IsTrue(a[7]);
+  const int silu = PyObject_IsTrue(a[8]);
+  if (need_dinit < 0 || silu < 0) return nullptr;
+  const at::Tensor& x = *px;
+  const at::Tensor& w = *pw;
+  const at::Tensor& dy = *pd;
+  const int64_t dev = x.get_device();
+  // The incoming gradients must sit on x's device and carry x's dtype (causal_conv1d.py's
+  // _check_grads and _ffi's checks, with their messages).
+  if (dy.get_device() != dev) return assertion("the gradient of out must be on the device of x");
+  if (pf && pf->get_device() != dev)
+    return assertion("the gradient of final_states must be on the device of x");
+  if (dy.scalar_type() != x.scalar_type() || (pf && pf->scalar_type() != x.scalar_type())) {
+    PyErr_SetString(PyExc_TypeError, "the gradients of out and final_states must have x's dtype");
+    return nullptr;
+  }
+  const int64_t B = x.size(0), T = x.size(1), D = x.size(2), W = w.size(1);
+  const int xdt = dtype_code(x.scalar_type()), wdt = dtype_code(w.scalar_type());
+  const int bdt = pb ? dtype_code(pb->scalar_type()) : 0;
+  const int idt = pi ? dtype_code(pi->scalar_type()) : 0;
+  if (xdt < 0 || wdt < 0 || bdt < 0 || idt < 0) {
+    PyErr_SetString(PyExc_TypeError, "unsupported dtype (fp32, fp16, bf16 or fp64 expected)");
+    return nullptr;
+  }
+  at::Tensor dx = at::empty({B, T, D}, x.options());
+  at::Tensor dw = at::empty_like(w);
+  at::Tensor db = pb ? at::empty_like(*pb) : at::Tensor();
+  at::Tensor di = need_dinit && pi ? at::empty_like(*pi) : at::Tensor();
+  const size_t ws_bytes = ccv1d_bwd_workspace_bytes(B, T, D, W, xdt);
+  at::Tensor ws = ws_bytes ? at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte))
+                           : at::Tensor();
+  void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev)).stream();
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = ccv1d_bwd(x.data_ptr(), x.stride(0), x.stride(1), xdt, w.data_ptr(), wdt,
+                 pb ? pb->data_ptr() : nullptr, bdt,
+                 ps ? static_cast<const int32_t*>(ps->data_ptr()) : nullptr,
+                 pi ? pi->data_ptr() : nullptr, idt, dy.data_ptr(), dy.stride(0), dy.stride(1),
+                 pf ? pf->data_ptr() : nullptr, dx.data_ptr(),
+                 di.defined() ? di.data_ptr() : nullptr, dw.data_ptr(),
+                 db.defined() ? db.data_ptr() : nullptr, ws.defined() ? ws.data_ptr() : nullptr,
+                 ws_bytes, B, T, D, W, silu, (int)dev, stream);
+  Py_END_ALLOW_THREADS
+  if (rc) return library_error(rc);
+  PyObject* r = PyTuple_New(4);
+  if (!r) return nullptr;
+  PyObject* items[4] = {THPVariable_Wrap(std::move(dx)), THPVariable_Wrap(std::move(dw)),
+                        wrap_or_none(std::move(db)), wrap_or_none(std::move(di))};
+  for (int i = 0; i < 4; ++i) {
+    if (!items[i]) {
+      for (int j = 0; j < 4; ++j) Py_XDECREF(items[j]);
+      Py_DECREF(r);
+      return nullptr;
+    }
+  }
+  for (int i = 0; i < 4; ++i) PyTuple_SET_ITEM(r, i, items[i]);
+  return r;
+}
+
+template <PyObject* (*IMPL)(PyObject* const*), Py_ssize_t N>
+PyObject* native_call(PyObject*, PyObject* const* a, Py_ssize_t n) {
+  if (n != N) {
+    PyErr_Format(PyExc_TypeError, "takes %zd arguments (%zd given)", N, n);
+    return nullptr;
+  }
+  try {
+    return IMPL(a);
+  } catch (const std::exception& e) {
+    PyErr_SetString(PyExc_RuntimeError, e.what());
+    return nullptr;
+  }
+}
+
 PyObject* native_set_error_type(PyObject*, PyObject* t) {
   if (!PyType_Check(t) || !PyType_IsSubtype(reinterpret_cast<PyTypeObject*>(t),
                                             reinterpret_cast<PyTypeObject*>(PyExc_Exception))) {
@@ -180,13 +318,18 @@ PyObject* native_set_error_type(PyObject*, PyObject* t) {
 PyMethodDef methods[] = {
     {"fwd", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(native_fwd)),
      METH_FASTCALL, "inference forward; None when the Python path must make the call"},
+    {"fwd_train",
+     reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(native_call<fwd_train_impl, 7>)),
+     METH_FASTCALL, "training forward on checked, canonicalised tensors; None for the Python path"},
+    {"bwd", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(native_call<bwd_impl, 9>)),
+     METH_FASTCALL, "backward of the autograd node; None for the Python path"},
     {"set_error_type", native_set_error_type, METH_O, "exception type for library errors"},
     {nullptr, nullptr, 0, nullptr},
 };
 
 PyModuleDef module = {
     PyModuleDef_HEAD_INIT, "_ccv1d_torch",
-    "Inference forward of causal_conv1d_fn over torch tensors in one native call", -1, methods,
+    "causal_conv1d_fn's passes over torch tensors, each in one native call", -1, methods,
     nullptr, nullptr, nullptr, nullptr,
 };
 

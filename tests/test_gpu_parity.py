@@ -415,6 +415,70 @@ def test_both_bindings_give_identical_results():
             assert torch.equal(a[k], b[k]), k
 
 
+@pytest.mark.parametrize("case", ["plain", "states", "seq", "fp32_no_bias", "strided_dout", "w20"])
+def test_native_training_passes_match_python_path(case):
+    """The autograd node's two passes go through the native calls of _ccv1d_torch (fwd_train,
+    bwd: allocation and launch in one call); the same passes made from Python through the ctypes
+    binding give identical outputs and gradients, bit for bit."""
+    from causal_conv1d_triton import _ffi
+
+    assert _ffi._torch_native is not None
+    B, T, D, W = 3, 300, 256, 20 if case == "w20" else 4
+    xdt = torch.float32 if case == "fp32_no_bias" else torch.bfloat16
+    inp = make_inputs(91, B, T, D, W, xdt=xdt, bias=case != "fp32_no_bias",
+                      init=case in ("states", "seq"),
+                      seq=varlen_seq(10, B, T, lo=20, hi=90) if case == "seq" else None)
+    final = case == "states"
+
+    def run():
+        x = inp["x"].to(DEV).requires_grad_(True)
+        w = inp["w"].to(DEV).requires_grad_(True)
+        b = None if inp["b"] is None else inp["b"].to(DEV).requires_grad_(True)
+        init = None if inp["init"] is None else inp["init"].to(DEV).requires_grad_(True)
+        seq = None if inp["seq"] is None else inp["seq"].to(DEV)
+        res = causal_conv1d_fn(x, w, b, seq_idx=seq, initial_states=init,
+                               return_final_states=final, activation="silu")
+        out, fin = res if final else (res, None)
+        dy = inp["dy"].to(DEV)
+        if case == "strided_dout":
+            big = torch.zeros(B, T, D + 8, dtype=dy.dtype, device=DEV)
+            big[..., 4:4 + D] = dy
+            dy = big[..., 4:4 + D]
+        outs, grads_out = [out], [dy]
+        if final:
+            outs.append(fin)
+            grads_out.append(inp["dfinal"].to(DEV))
+        wrt = [t for t in (x, w, b, init) if t is not None]
+        grads = torch.autograd.grad(outs, wrt, grads_out)
+        return [out.detach()] + ([fin.detach()] if final else []) + list(grads)
+
+    got = run()
+    native, _ffi._native = _ffi._native, None
+    torch_native, _ffi._torch_native = _ffi._torch_native, None
+    try:
+        want = run()
+    finally:
+        _ffi._native = native
+        _ffi._torch_native = torch_native
+    torch.cuda.synchronize()
+    assert len(got) == len(want)
+    for g, wnt in zip(got, want):
+        assert g.dtype == wnt.dtype and torch.equal(g, wnt)
+
+
+def test_native_backward_refuses_foreign_gradients():
+    """The native backward refuses a gradient of out on another device (a host address would
+    reach a kernel) or of another dtype than x, before any launch."""
+    from causal_conv1d_triton import causal_conv1d as cc
+
+    inp = make_inputs(92, 2, 64, 128, 4)
+    x, w, b = inp["x"].to(DEV), inp["w"].to(DEV), inp["b"].to(DEV)
+    with pytest.raises(AssertionError, match="gradient of out must be on the device of x"):
+        cc._bwd(x, w, b, None, None, inp["dy"], None, False, True)
+    with pytest.raises(TypeError):
+        cc._bwd(x, w, b, None, None, inp["dy"].to(DEV).float(), None, False, True)
+
+
 @pytest.mark.parametrize("case", ["plain", "states", "seq_int64", "strided", "final_out",
                                   "generic", "empty"])
 def test_native_inference_forward_matches_python_path(case):
@@ -448,10 +512,12 @@ def test_native_inference_forward_matches_python_path(case):
                                activation="silu")
         fin = torch.empty(B, W - 1, D, dtype=x.dtype, device=DEV) if final else None
         native, _ffi._native = _ffi._native, None
+        torch_native, _ffi._torch_native = _ffi._torch_native, None
         try:
             want = _fwd(x, w, b, None if seq is None else seq.int(), init, fin, True)
         finally:
             _ffi._native = native
+            _ffi._torch_native = torch_native
     torch.cuda.synchronize()
     if final:
         assert torch.equal(got[0], want) and torch.equal(got[1], fin)
