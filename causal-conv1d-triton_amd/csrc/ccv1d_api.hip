@@ -68,6 +68,11 @@ FastShape shape_of(int x_dt) {
 // Every tile is at least min_tile_rows(W) long (defaults and overrides), longer than the window
 // (W - 1), so only the first tile of a row has a window outside x.
 constexpr int kMaxTileRows = 64;
+// Longest tile without seq_idx for the backward with one channel per lane and the forward from
+// kFwdTileRows128W (see bwd_tiling_for, fwd_tiling_for); with seq_idx a tile and both halos must fit
+// one RowIds, which keeps kMaxTileRows.
+constexpr int kMaxTileRowsLong = 128;
+constexpr int kFwdTileRows128W = 24;
 constexpr int kMinTileRows = 8;
 static_assert(kMaxTileRows + 2 * (kMaxFastW - 1) <= kRowIds, "tile and halos must fit one RowIds");
 static_assert(kMaxFastW <= kMaxTileRows, "the longest tile must be longer than every window");
@@ -193,11 +198,17 @@ Tiling fast_tiling(int64_t B, int64_t T, int64_t D, int vec, int nw, int lmin, i
 // D=1024 forward 7.0 -> 5.3 us; B=4 T=2048, whose 16-row grid has 256 workgroups, stays at 16).
 constexpr int64_t kFwdSmallGrid = 256;
 
-Tiling fwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw) {
+// The forward from width kFwdTileRows128W without seq_idx takes tiles of up to kMaxTileRowsLong
+// rows (its window of W - 1 halo rows is re-read per tile). Measured (forward alone, bf16, 64
+// against 128 rows): B=4 T=8192 D=1024 W=24 40.4 -> 39.8 us, W=32 48.5 -> 46.8; B=8 T=4096 D=4096
+// W=24 153.5 -> 146.6, W=32 181.9 -> 169.5; B=4 T=1024 D=8192 W=32 49.4 -> 47.2; at widths 17-20
+// mixed (B=16 T=2048 D=2048 W=17 63.7 against 69.7 with 128 rows).
+Tiling fwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw, bool seq) {
   const int lmin = min_tile_rows(W);
   const int over = tune().fwd_rows >= lmin ? tune().fwd_rows : 0;
   const int64_t min_time_wg = W >= kFwdLongTileW ? 1 : kMinTimeWorkgroups;
-  Tiling t = fast_tiling(B, T, D, cpl, nw, lmin > 16 ? lmin : 16, kMaxTileRows, kTargetWaves, over,
+  const int lmax = W >= kFwdTileRows128W && !seq ? kMaxTileRowsLong : kMaxTileRows;
+  Tiling t = fast_tiling(B, T, D, cpl, nw, lmin > 16 ? lmin : 16, lmax, kTargetWaves, over,
                          min_time_wg);
   if (over == 0 && t.L == 16 && lmin < 16 && t.nBlk < kFwdSmallGrid)
     t = fast_tiling(B, T, D, cpl, nw, lmin, lmin, kTargetWaves, lmin);
@@ -228,15 +239,15 @@ FastShape fwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
   } else if (W >= kFwdWideW) {
     sh.cpl = fwd_cpl_small(x_dt);
   } else if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
-    const Tiling t = fwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);
+    const Tiling t = fwd_tiling_for(B, T, D, W, sh.cpl, sh.nw, false);
     if (D % sh.cpl || B * t.nT * t.nGW < kTargetWaves) sh.cpl = fwd_cpl_small(x_dt);
   }
   return sh;
 }
 
-Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
+Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt, bool seq) {
   const FastShape sh = fwd_shape(x_dt, B, T, D, W);
-  return fwd_tiling_for(B, T, D, W, sh.cpl, sh.nw);
+  return fwd_tiling_for(B, T, D, W, sh.cpl, sh.nw, seq);
 }
 
 // Workgroups below which the backward halves its tiles (down to kMinTileRows): a grid with fewer
@@ -246,14 +257,12 @@ Tiling fwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt) {
 // shape (512 workgroups) keeps 32 rows.
 constexpr int64_t kBwdSmallGrid = 256;
 
-// Longest tile of the backward with one channel per lane (kCplLong) and no seq_idx: halving the
-// tiles' count halves the work each tile spends outside the pipelined loop (its halo rows, the g
-// rows handed between waves, the partial dweight row), which grows with the width. Measured
-// (fwd+bwd step, bf16, B=4 T=8192 D=1024, 64 against 128 rows in the backward): W=12 83.1 -> 80.7
-// us, W=16 97.9 -> 93.4, W=20 117.1 -> 114.1, W=24 149.6 -> 133.3, W=32 190.5 -> 166.5 (the
-// forward gained nothing from 128-row tiles). With seq_idx a tile and both halos must fit one
-// RowIds, which keeps kMaxTileRows.
-constexpr int kMaxTileRowsLong = 128;
+// The backward with one channel per lane (kCplLong) and no seq_idx takes tiles of up to
+// kMaxTileRowsLong rows: halving the tiles' count halves the work each tile spends outside the
+// pipelined loop (its halo rows, the g rows handed between waves, the partial dweight row), which
+// grows with the width. Measured (fwd+bwd step, bf16, B=4 T=8192 D=1024, 64 against 128 rows in the
+// backward): W=12 83.1 -> 80.7 us, W=16 97.9 -> 93.4, W=20 117.1 -> 114.1, W=24 149.6 -> 133.3,
+// W=32 190.5 -> 166.5.
 
 Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw, bool seq) {
   const int lmin = min_tile_rows(W);
@@ -450,7 +459,7 @@ int fwd_entry(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   Tiling tl{};
   if (T > 0) {
     if (fast) {
-      tl = fwd_fast_tiling(B, T, D, W, x_dtype);
+      tl = fwd_fast_tiling(B, T, D, W, x_dtype, seq_idx != nullptr);
     } else {
       tl = generic_tiling(T);
       if (B * tl.nT >= (int64_t(1) << 31) || cdiv(D, 64) > 65535)

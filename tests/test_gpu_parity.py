@@ -787,18 +787,21 @@ def _cols(D, n, seed):
     (24, 1024, 3072, 16, torch.float16, False),
     (6, 2048, 4096, 20, torch.bfloat16, False),  # width 20: 2-row batches
     (8, 1024, 4096, 24, torch.float32, True),
-    (4, 1024, 8192, 32, torch.bfloat16, False),
+    (4, 1024, 8192, 32, torch.bfloat16, False),  # 128-row tiles in both passes
+    (8, 2048, 4096, 28, torch.float16, False),
 ])
 def test_mid_size_long_tiles(B, T, D, W, xdt, seq):
     """Shapes where the backward (2 or 1 channels per lane) and the forward from width 12 take
-    64-row tiles however few workgroups that leaves along time, and where the backward with one
-    channel per lane and no seq_idx takes 128-row tiles (widths 16, 20 and 32 here): a channel
-    subset against the oracle, with initial states and their gradient."""
+    64-row tiles however few workgroups that leaves along time, and where, without seq_idx, the
+    backward with one channel per lane takes 128-row tiles (widths 16, 20, 28 and 32 here) and the
+    forward from width 24 too (28 and 32): a channel subset against the oracle, with initial
+    states and their gradient, and final states and theirs where seq_idx allows them."""
     s = varlen_seq(B + W, B, T, lo=64, hi=1024, pad_frac=0.05) if seq else None
     inp = make_inputs(B * 100 + W, B, T, D, W, xdt=xdt, init=True, seq=s)
-    gpu = run_gpu(inp, "silu", init_grad=True)
+    gpu = run_gpu(inp, "silu", return_final=not seq, dfinal=not seq, init_grad=True)
     cols = _cols(D, 24, W)
-    compare(gpu, oracle_ref(inp, True, cols=cols, need_dinit=True), True, cols=cols)
+    ref = oracle_ref(inp, True, cols=cols, final=not seq, dfinal=not seq, need_dinit=True)
+    compare(gpu, ref, True, cols=cols)
     if seq:
         assert torch.all(gpu["out"][s < 0] == 0) and torch.all(gpu["dx"][s < 0] == 0)
 
