@@ -466,6 +466,49 @@ def test_native_training_passes_match_python_path(case):
         assert g.dtype == wnt.dtype and torch.equal(g, wnt)
 
 
+@pytest.mark.parametrize("W", [4, 12, 24])
+@pytest.mark.parametrize("axis", ["time", "batch"])
+def test_zero_stride_inputs_and_gradients(W, axis):
+    """Expanded views (stride 0 along time or batch, unit channel stride) are read in place: x
+    broadcast over one axis, and the gradient of out as autograd hands it over for a sum over that
+    axis. Outputs and gradients equal those of the materialised copies bit for bit, through the
+    native passes and through the ctypes path."""
+    from causal_conv1d_triton import _ffi
+
+    B, T, D = 3, 200, 96
+    g = _gen(400 + W)
+    shape = (B, 1, D) if axis == "time" else (1, T, D)
+    x_small = torch.randn(*shape, generator=g).to(torch.bfloat16).to(DEV)
+    r_small = torch.randn(*shape, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(D, W, generator=g) / math.sqrt(W)).to(DEV)
+    b = torch.randn(D, generator=g).to(DEV)
+    x_exp = x_small.expand(B, T, D)
+    dy_exp = r_small.expand(B, T, D)
+    assert x_exp.stride(1 if axis == "time" else 0) == 0 and x_exp.stride(2) == 1
+    assert dy_exp.stride(1 if axis == "time" else 0) == 0
+
+    def run(x, dy):
+        x = x.detach().requires_grad_(True)
+        wr, br = w.detach().requires_grad_(True), b.detach().requires_grad_(True)
+        out = causal_conv1d_fn(x, wr, br, activation="silu")
+        grads = torch.autograd.grad(out, (x, wr, br), dy)
+        return [out.detach()] + list(grads)
+
+    want = run(x_exp.contiguous(), dy_exp.contiguous())
+    got = run(x_exp, dy_exp)
+    native, _ffi._native = _ffi._native, None
+    torch_native, _ffi._torch_native = _ffi._torch_native, None
+    try:
+        got_py = run(x_exp, dy_exp)
+    finally:
+        _ffi._native = native
+        _ffi._torch_native = torch_native
+    torch.cuda.synchronize()
+    for name, gv, pv, wv in zip(("out", "dx", "dweight", "dbias"), got, got_py, want):
+        assert torch.equal(gv, wv), name
+        assert torch.equal(pv, wv), name
+
+
 def test_native_backward_refuses_foreign_gradients():
     """The native backward refuses a gradient of out on another device (a host address would
     reach a kernel) or of another dtype than x, before any launch."""
