@@ -363,11 +363,11 @@ __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBu
 // with alternating directions both tiles read those rows at about the same time (both at their
 // start, or both at their end), so the second read finds them in L2 instead of memory.
 //
-// 16-bit instances without seq_idx are compiled for 4 waves per SIMD (at most 128 VGPRs): widths 8
-// and 16 need 132 and 134 otherwise, which leaves one 8-wave workgroup per CU (B=4 T=8192 D=1024
-// forward W=8 33.8 -> 31.4 us, W=16 42.2 -> 34.9 us; B=8 T=4096 D=5376 W=8 150.6 -> 144.2 us; 2
-// VGPRs spill in each). The other widths already fit; the seq_idx and fp32 instances would spill
-// more, so they keep the default bound.
+// 16-bit instances without seq_idx are compiled for 4 waves per SIMD (at most 128 VGPRs): width 16
+// (2 channels per lane) needs 134 otherwise, which leaves one 8-wave workgroup per CU (B=4 T=8192
+// D=1024 forward 42.2 -> 34.9 us; 2 VGPRs spill), as did width 8 when it took 4 channels per lane.
+// The other widths already fit; the seq_idx and fp32 instances would spill more, so they keep the
+// default bound.
 template <typename TX, int W, bool SEQ>
 constexpr int fwd_waves_per_simd() {
   return (sizeof(TX) == 2 && !SEQ) ? 4 : 2;

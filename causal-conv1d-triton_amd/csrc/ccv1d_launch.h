@@ -56,7 +56,14 @@ template <typename TX> struct BwdCfg {
   static constexpr int DXST = sizeof(TX) == 2 ? kCacheSC1NT : kCacheNT;
 };
 constexpr int kMaxFastW = 32;    // widths 2..kMaxFastW have register-window kernels
-constexpr int kFwdWideW = 9;     // first width whose forward always uses FwdCfg::CPL_SMALL
+// The forward takes 2 channels per lane from width 7: with 4, widths 7 and 8 need 118-132 VGPRs
+// (4 waves per SIMD at most), with 2 they need about 70 and the short-tile grids of mid-size shapes
+// gain the most (forward alone at W=8: B=32 T=1024 D=2048 73.9 -> 54.3 us, B=4 T=1024 D=8192 37.7
+// -> 31.2; fwd+bwd step at B=4 T=8192 D=1024: W=7 68.8 -> 67.6 us, W=8 71.4 -> 69.9). At widths 5
+// and 6 the 4-channel forward was faster at B=4 T=8192 D=1024 (forward alone 28.4 against 29.7 us
+// at W=5, 28.8 against 29.6 at W=6) and on large grids with 32-row tiles (B=8 T=4096 D=4096 W=6
+// 98.9 against 105.0 us), so they keep 4.
+constexpr int kFwdWideW = 7;     // first width whose forward always uses FwdCfg::CPL_SMALL
 constexpr int kBwdWideW = 6;     // first width whose backward uses BwdCfg::CPL_WIDE
 // One channel per lane (kCplLong) from width kFwdLongW in the forward and from kBwdLongW in the
 // backward. From width 17 the weights, the windows and the dweight sums of W taps per channel fit

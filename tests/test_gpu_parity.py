@@ -866,7 +866,9 @@ def test_config2_readme_sweep(T, variant):
     (4, 4096, 1024, 5, torch.float16),   # the same split at width 5 (backward with 4-row batches)
     (4, 2048, 1002, 4, torch.bfloat16),  # dim not a multiple of 4: both passes 2 channels per lane
     (1, 512, 262, 5, torch.float16),     # the same on a small grid at width 5
-    (4, 8192, 1024, 8, torch.bfloat16),  # width 8: 4-waves forward, 2-channel 4-row backward
+    (4, 8192, 1024, 6, torch.bfloat16),  # width 6: the widest 4-channel forward, 2-channel backward
+    (4, 8192, 1024, 7, torch.float16),   # width 7: both passes 2 channels per lane
+    (4, 8192, 1024, 8, torch.bfloat16),  # width 8: the same, 4-row backward batches
 ])
 def test_channels_per_lane_choices(B, T, D, W, xdt):
     """Shapes on either side of the host's choice of 4 or 2 channels per lane in each pass, with
