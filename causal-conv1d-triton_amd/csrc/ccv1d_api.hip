@@ -229,9 +229,17 @@ int fwd_cpl_small(int x_dt) {
 // D=1024 T=512 5.23 -> 4.68 us, T=2048 8.47 -> 8.11; B=16 D=2048 chunks of T=256 9.36 -> 9.04 us
 // per call, decode steps 2.56 -> 2.53. Grids that reach the target keep 4 channels (benchmark shape
 // 29.5 against 31.8 us; B=2 T=8192 D=1024 13.3 against 14.0). fp32 x follows the same rule in both
-// passes (fwd+bwd step, B=4 D=1024 W=4: T=512 19.1 -> 16.8 us, T=2048 39.9 -> 37.7). From width
-// kFwdWideW up the forward always takes CPL_SMALL (its weights and window are per channel), from
-// kFwdLongW up kCplLong.
+// passes (fwd+bwd step, B=4 D=1024 W=4: T=512 19.1 -> 16.8 us, T=2048 39.9 -> 37.7). 16-bit x
+// also takes CPL_SMALL where the CPL grid reaches the target only with tiles shorter than
+// kFwdShortTile rows: each workgroup then spends much of its short life on its start (halo, taps,
+// first batch), which twice the resident workgroups hide. Measured (bf16, widths 4-6, 2 against 4
+// channels, 16-row tiles in both): forward alone 3-23 % faster on 9 of 10 mid-size shapes (B=32
+// T=1024 D=2048 W=4 65.5 -> 50.3 us, B=8 T=1024 D=4096 W=4 31.7 -> 28.0), up to 5 % slower on the
+// tenth (B=16 T=512 D=4096), and the fwd+bwd step 1.3-11 % faster on all ten; fp32 x (16- against
+// 8-byte rows) was mixed (-15 % to +6 %) and keeps 4. From width kFwdWideW up the forward always
+// takes CPL_SMALL (its weights and window are per channel), from kFwdLongW up kCplLong.
+constexpr int kFwdShortTile = 32;
+
 FastShape fwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
   FastShape sh = shape_of<FwdCfg>(x_dt);
   if (W >= kFwdLongW) {
@@ -240,7 +248,8 @@ FastShape fwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
     sh.cpl = fwd_cpl_small(x_dt);
   } else if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
     const Tiling t = fwd_tiling_for(B, T, D, W, sh.cpl, sh.nw, false);
-    if (D % sh.cpl || B * t.nT * t.nGW < kTargetWaves) sh.cpl = fwd_cpl_small(x_dt);
+    if (D % sh.cpl || B * t.nT * t.nGW < kTargetWaves || (esize(x_dt) == 2 && t.L < kFwdShortTile))
+      sh.cpl = fwd_cpl_small(x_dt);
   }
   return sh;
 }

@@ -866,6 +866,9 @@ def test_config2_readme_sweep(T, variant):
     (4, 4096, 1024, 5, torch.float16),   # the same split at width 5 (backward with 4-row batches)
     (4, 2048, 1002, 4, torch.bfloat16),  # dim not a multiple of 4: both passes 2 channels per lane
     (1, 512, 262, 5, torch.float16),     # the same on a small grid at width 5
+    (8, 1024, 4096, 4, torch.bfloat16),  # 16-row forward tiles: 2 channels in the forward, 4 back
+    (8, 1024, 2048, 6, torch.float16),   # the same at width 6 (2 channels in both passes)
+    (8, 1024, 2048, 4, torch.float32),   # fp32 keeps 4 channels on 16-row forward tiles
     (4, 8192, 1024, 6, torch.bfloat16),  # width 6: the widest 4-channel forward, 2-channel backward
     (4, 8192, 1024, 7, torch.float16),   # width 7: both passes 2 channels per lane
     (4, 8192, 1024, 8, torch.bfloat16),  # width 8: the same, 4-row backward batches
