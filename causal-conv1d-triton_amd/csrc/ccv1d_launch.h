@@ -62,7 +62,8 @@ constexpr int kMaxFastW = 32;    // widths 2..kMaxFastW have register-window ker
 // -> 31.2; fwd+bwd step at B=4 T=8192 D=1024: W=7 68.8 -> 67.6 us, W=8 71.4 -> 69.9). At widths 5
 // and 6 the 4-channel forward was faster at B=4 T=8192 D=1024 (forward alone 28.4 against 29.7 us
 // at W=5, 28.8 against 29.6 at W=6) and on large grids with 32-row tiles (B=8 T=4096 D=4096 W=6
-// 98.9 against 105.0 us), so they keep 4.
+// 98.9 against 105.0 us), so they keep 4 there (fwd_shape in ccv1d_api.hip still gives 16-bit x 2
+// channels on the grids where 4 would take 16-row tiles).
 constexpr int kFwdWideW = 7;     // first width whose forward always uses FwdCfg::CPL_SMALL
 constexpr int kBwdWideW = 6;     // first width whose backward uses BwdCfg::CPL_WIDE
 // One channel per lane (kCplLong) from width kFwdLongW in the forward and from kBwdLongW in the
