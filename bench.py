@@ -306,7 +306,7 @@ def run_configs(dev, widths=False, only=None, shapes=False):
     shape (bf16, bias + silu) at every width the vectorised kernels cover, forward alone and
     forward + backward (widths 2-8, 9, 12, 16, 17, 20, 24 and 32). With `shapes`, instead: the
     same two passes over mid-size shapes (many batch rows or short sequences, where the tiling's
-    choice of tile length matters) at widths 4-9, 12, 16 and 24.
+    choice of tile length matters) at widths 2-9, 12, 16 and 24.
 
     `only` (a set of strings, e.g. {"2:512", "5:7"} or, with `widths`, {"8"}) restricts the run to
     the named configurations (N, or N:T for configuration 2's lengths, N:W for configuration 5's
@@ -387,7 +387,7 @@ def run_configs(dev, widths=False, only=None, shapes=False):
                      torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
                     for _ in range(nsets)]
             b = torch.randn(D, generator=gen, device=dev).requires_grad_(True)
-            for W in (4, 5, 6, 7, 8, 9, 12, 16, 24):
+            for W in (2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 24):
                 if only and str(W) not in only:
                     continue
                 w = (torch.randn(D, W, generator=gen, device=dev) / math.sqrt(W)).requires_grad_(True)
@@ -568,7 +568,7 @@ def main():
     ap.add_argument("--widths", action="store_true",
                     help="instead of the headline line, the benchmark shape at widths 2-32")
     ap.add_argument("--shapes", action="store_true",
-                    help="instead of the headline line, mid-size shapes at widths 4-24")
+                    help="instead of the headline line, mid-size shapes at widths 2-24")
     ap.add_argument("--only", default="",
                     help="with --configs, --widths or --shapes: comma-separated workloads to run "
                          "(e.g. 2:512,5:7 or, with --widths or --shapes, widths such as 8)")

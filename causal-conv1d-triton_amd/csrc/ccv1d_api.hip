@@ -232,10 +232,10 @@ int fwd_cpl_small(int x_dt) {
 // passes (fwd+bwd step, B=4 D=1024 W=4: T=512 19.1 -> 16.8 us, T=2048 39.9 -> 37.7). 16-bit x
 // also takes CPL_SMALL where the CPL grid reaches the target only with tiles shorter than
 // kFwdShortTile rows: each workgroup then spends much of its short life on its start (halo, taps,
-// first batch), which twice the resident workgroups hide. Measured (bf16, widths 4-6, 2 against 4
-// channels, 16-row tiles in both): forward alone 3-23 % faster on 9 of 10 mid-size shapes (B=32
+// first batch), which twice the resident workgroups hide. Measured (bf16, widths 2-6, 2 against 4
+// channels, 16-row tiles in both): forward alone 3-27 % faster on 9 of 10 mid-size shapes (B=32
 // T=1024 D=2048 W=4 65.5 -> 50.3 us, B=8 T=1024 D=4096 W=4 31.7 -> 28.0), up to 5 % slower on the
-// tenth (B=16 T=512 D=4096), and the fwd+bwd step 1.3-11 % faster on all ten; fp32 x (16- against
+// tenth (B=16 T=512 D=4096), and the fwd+bwd step 1-11 % faster on all ten; fp32 x (16- against
 // 8-byte rows) was mixed (-15 % to +6 %) and keeps 4. From width kFwdWideW up the forward always
 // takes CPL_SMALL (its weights and window are per channel), from kFwdLongW up kCplLong.
 constexpr int kFwdShortTile = 32;
