@@ -254,8 +254,9 @@ def causal_conv1d_fn(
         xx = cat(initial_states, x) along time
 
     Arguments:
-      x: (batch, seqlen, dim) on a GPU, fp32/fp16/bf16, unit stride along dim (other strides are
-         free; a tensor without one is copied first).
+      x: (batch, seqlen, dim) on a GPU, bf16/fp16/fp32 (or fp64, on the scalar kernels), unit
+         stride along dim (other strides, zero included, are free; a tensor without one is
+         copied first).
       weight: (dim, width) with width >= 2, any float dtype; dweight comes back in that dtype.
       bias: optional (dim,).
       seq_idx: optional (batch, seqlen) integer ids marking packed sequences: a tap only reaches
