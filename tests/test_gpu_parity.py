@@ -698,6 +698,30 @@ def test_empty_inputs(shape):
         assert torch.equal(init.grad, dfin.to(init.dtype))
 
 
+@pytest.mark.parametrize("W,xdt", [(3, torch.float16), (4, torch.bfloat16), (6, torch.bfloat16)])
+def test_forward_channel_choices_agree(W, xdt):
+    """The forward's channels per lane and tile length depend on the shape: (2, 8192, 2048) runs
+    4 channels per lane on 32-row tiles, its first 1024 rows alone (a small grid) 2 channels, and
+    16 copies of those rows 2 channels on the 16-row tiles the 4-channel tiling would take. Each
+    output row depends only on rows up to it, so all three give the same first 1024 rows bit for
+    bit (silu and bias included), and those match the oracle on a channel subset."""
+    B, T, D, T0 = 2, 8192, 2048, 1024
+    inp = make_inputs(60 + W, B, T, D, W, xdt=xdt)
+    x, w, b = inp["x"].to(DEV), inp["w"].to(DEV), inp["b"].to(DEV)
+    with torch.no_grad():
+        long = causal_conv1d_fn(x, w, b, activation="silu")[:, :T0]
+        prefix = causal_conv1d_fn(x[:, :T0].contiguous(), w, b, activation="silu")
+        stacked = causal_conv1d_fn(x[:, :T0].repeat(8, 1, 1), w, b, activation="silu")
+    torch.cuda.synchronize()
+    assert torch.equal(long, prefix)
+    assert torch.equal(stacked, prefix.repeat(8, 1, 1))
+    cols = _cols(D, 8, W)
+    sub = {"x": inp["x"][:, :T0], "w": inp["w"], "b": inp["b"], "init": None,
+           "dy": inp["dy"][:, :T0], "dfinal": inp["dfinal"], "seq": None}
+    ref = oracle_ref(sub, True, cols=cols, bwd=False)
+    check_lowp(_sub(prefix.cpu(), cols), ref["out"], False, "out")
+
+
 @pytest.mark.parametrize("case", ["cached", "seq_states", "streamed"])
 def test_forward_cache_policies_leave_results_unchanged(case):
     """The forward picks its load/store cache policies and, for streaming inference calls, its
