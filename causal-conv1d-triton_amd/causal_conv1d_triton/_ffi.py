@@ -81,6 +81,14 @@ def load() -> ctypes.CDLL:
     lib.ccv1d_time_main_kernel.argtypes = [_c_ptr, _c_ptr]
     lib.ccv1d_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.ccv1d_bwd_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]
+    lib.ccv1d_bwd_workspace_bytes_for.restype = ctypes.c_size_t
+    lib.ccv1d_bwd_workspace_bytes_for.argtypes = [
+        _c_ptr, _c_i64, _c_i64, _c_int,  # x, strides, dtype
+        _c_ptr,  # seq_idx
+        _c_ptr, _c_i64, _c_i64,  # dout, strides
+        _c_ptr, _c_ptr,  # dfinal_states, dx
+        _c_i64, _c_i64, _c_i64, _c_i64,  # batch, seqlen, dim, width
+    ]
     lib.ccv1d_bwd.restype = _c_int
     lib.ccv1d_bwd.argtypes = [
         _c_ptr, _c_i64, _c_i64, _c_int,  # x
@@ -173,7 +181,17 @@ def time_main_kernel(start, stop) -> None:
 
 
 def bwd_workspace_bytes(B: int, T: int, D: int, W: int, x_dtype: torch.dtype) -> int:
+    """Upper bound of the backward's workspace over every path a shape can take."""
     return load().ccv1d_bwd_workspace_bytes(B, T, D, W, DTYPE_CODES.get(x_dtype, 0))
+
+
+def bwd_workspace_bytes_for(x, seq_idx, dout, dfinal_states, dx, W: int) -> int:
+    """Workspace of the path ccv1d_bwd takes for these tensors (dx contiguous)."""
+    B, T, D = x.shape
+    return load().ccv1d_bwd_workspace_bytes_for(
+        x.data_ptr(), x.stride(0), x.stride(1), _code(x), _ptr(seq_idx),
+        dout.data_ptr(), dout.stride(0), dout.stride(1), _ptr(dfinal_states), dx.data_ptr(),
+        B, T, D, W)
 
 
 def _bwd_args(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit, dweight,

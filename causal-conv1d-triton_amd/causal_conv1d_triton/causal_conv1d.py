@@ -47,13 +47,20 @@ def _check_inputs(x, weight, bias, seq_idx, initial_states):
     assert (T + W) * (st if st > D else D) < 2**31, "seqlen * dim too large for 32-bit offsets"
 
 
-def _check_grads(x, dout, dfinal_states):
+def _check_grads(x, width, dout, dfinal_states):
     """The backward's incoming gradients must sit on x's device (the reference's launcher refuses
-    host tensors; here their addresses would reach a kernel)."""
+    host tensors; here their addresses would reach a kernel) and have the shapes of out and of the
+    final states: the library reads batch * seqlen * dim elements of dout and batch * (width - 1)
+    * dim of dfinal_states, so a smaller tensor would be read past its end."""
     dev = x.get_device()
     assert dout.get_device() == dev, "the gradient of out must be on the device of x"
-    assert dfinal_states is None or dfinal_states.get_device() == dev, (
-        "the gradient of final_states must be on the device of x")
+    assert dout.shape == x.shape, "the gradient of out must have the shape of x"
+    if dfinal_states is not None:
+        assert dfinal_states.get_device() == dev, (
+            "the gradient of final_states must be on the device of x")
+        B, _, D = x.shape
+        assert dfinal_states.shape == (B, width - 1, D), (
+            "the gradient of final_states must be (batch, width - 1, dim)")
 
 
 def _channels_contiguous(t: Tensor) -> Tensor:
@@ -87,14 +94,14 @@ def _bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, need_din
                                      need_dinit, silu)
         if res is not None:
             return res
-    _check_grads(x, dout, dfinal_states)
     B, T, D = x.shape
     W = weight.shape[1]
+    _check_grads(x, W, dout, dfinal_states)
     dx = torch.empty(B, T, D, device=x.device, dtype=x.dtype)
     dinit = torch.empty_like(initial_states) if need_dinit else None
     dweight = torch.empty_like(weight)
     dbias = torch.empty_like(bias) if bias is not None else None
-    nbytes = _ffi.bwd_workspace_bytes(B, T, D, W, x.dtype)
+    nbytes = _ffi.bwd_workspace_bytes_for(x, seq_idx, dout, dfinal_states, dx, W)
     workspace = torch.empty(nbytes, device=x.device, dtype=torch.uint8) if nbytes else None
     _ffi.bwd(x, weight, bias, seq_idx, initial_states, dout, dfinal_states, dx, dinit, dweight,
              dbias, workspace, silu)

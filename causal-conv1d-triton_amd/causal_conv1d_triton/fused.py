@@ -49,7 +49,6 @@ def causal_conv1d_bwd(
         assert dfinal_states is None, "cannot take final-state gradients if seq_idx is not None"
     if return_dinitial_states:
         assert initial_states is not None, "return_dinitial_states requires initial_states"
-    assert dout.shape == x.shape, "dout must have the shape of x"
     x = _channels_contiguous(x)
     dout = _channels_contiguous(dout)
     weight = weight.contiguous()
@@ -57,10 +56,9 @@ def causal_conv1d_bwd(
     seq_idx = seq_idx.to(torch.int32).contiguous() if seq_idx is not None else None
     initial_states = initial_states.contiguous() if initial_states is not None else None
     dfinal_states = dfinal_states.contiguous() if dfinal_states is not None else None
-    _check_grads(x, dout, dfinal_states)
-
     B, T, D = x.shape
     W = weight.shape[1]
+    _check_grads(x, W, dout, dfinal_states)
     if dx is None:
         dx = torch.empty(B, T, D, device=x.device, dtype=x.dtype)
     else:

@@ -629,6 +629,45 @@ struct BwdPlan {
   size_t need = 0;     // workspace bytes the launches use
 };
 
+// Kernels, tiling and workspace of a backward with these rows (B, T, D > 0): the vectorised
+// kernels when the x dtype, the width and the alignment of every row of x, dout and dx (and of
+// dfinal_states) allow them, else the generic ones.
+struct BwdPath {
+  bool fast = false;
+  bool wide = false;   // generic path above kMaxGenericW: g goes through the workspace
+  Tiling tl{};
+  int64_t rows = 0;    // partial rows of dweight/dbias
+  size_t g_off = 0;    // byte offset of the g buffer in the workspace (wide)
+  size_t need = 0;     // workspace bytes
+};
+
+BwdPath bwd_path(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype, bool seq,
+                 const void* dout, int64_t dout_stride_b, int64_t dout_stride_t,
+                 const void* dfinal_states, const void* dx, int64_t dx_stride_b,
+                 int64_t dx_stride_t, bool ws_aligned, int64_t B, int64_t T, int64_t D,
+                 int64_t W) {
+  BwdPath r;
+  const int bcpl = bwd_shape(x_dtype, B, T, D, W).cpl;
+  r.fast = fast_dtype(x_dtype, W) && rows_ok(x_dtype, bcpl, T, D, x, x_stride_b, x_stride_t) &&
+           rows_ok(x_dtype, bcpl, T, D, dout, dout_stride_b, dout_stride_t) &&
+           rows_ok(x_dtype, bcpl, T, D, dx, dx_stride_b, dx_stride_t) &&
+           (!dfinal_states || aligned_to(dfinal_states, bcpl * esize(x_dtype))) && ws_aligned;
+  if (r.fast) {
+    r.tl = bwd_fast_tiling(B, T, D, W, x_dtype, seq);
+    r.rows = B * r.tl.nTB;
+  } else {
+    r.tl = generic_tiling(T);
+    r.rows = B * r.tl.nT;
+    r.wide = W > kMaxGenericW;
+  }
+  r.need = partial_bytes(r.rows, W, D);
+  if (r.wide) {
+    r.g_off = g_buffer_offset(r.need);
+    r.need = r.g_off + g_buffer_bytes(B, T, D);
+  }
+  return r;
+}
+
 // `ws_aligned`: the workspace the call will use is 16-byte aligned (the vectorised backward stores
 // partial rows with 16-byte accesses).
 // dx_stride_b / dx_stride_t: strides of dx in elements (T * D and D for a contiguous dx).
@@ -714,31 +753,22 @@ int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
   r.has_bias = bias != nullptr;
   if (pl.skip || pl.empty) return CCV1D_OK;
 
-  const int bcpl = bwd_shape(x_dtype, B, T, D, W).cpl;
-  pl.fast = fast_dtype(x_dtype, W) && rows_ok(x_dtype, bcpl, T, D, x, x_stride_b, x_stride_t) &&
-            rows_ok(x_dtype, bcpl, T, D, dout, dout_stride_b, dout_stride_t) &&
-            rows_ok(x_dtype, bcpl, T, D, dx, dx_stride_b, dx_stride_t) &&
-            (!dfinal_states || aligned_to(dfinal_states, bcpl * esize(x_dtype))) && ws_aligned;
-  int64_t rows;
+  const BwdPath path = bwd_path(x, x_stride_b, x_stride_t, x_dtype, seq_idx != nullptr, dout,
+                                dout_stride_b, dout_stride_t, dfinal_states, dx, dx_stride_b,
+                                dx_stride_t, ws_aligned, B, T, D, W);
+  pl.fast = path.fast;
+  pl.wide = path.wide;
+  p.tl = path.tl;
   if (pl.fast) {
-    p.tl = bwd_fast_tiling(B, T, D, W, x_dtype, seq_idx != nullptr);
-    rows = B * p.tl.nTB;
     p.x_bytes = slab_bytes(x_dtype, T, D, x_stride_t);
     p.y_bytes = slab_bytes(x_dtype, T, D, dout_stride_t);
     p.o_bytes = slab_bytes(x_dtype, T, D, dx_stride_t);
-  } else {
-    p.tl = generic_tiling(T);
-    rows = B * p.tl.nT;
-    if (rows >= (int64_t(1) << 31) || cdiv(D, 64) > 65535)
-      return fail(CCV1D_ERR_UNSUPPORTED, "shape too large for the generic kernel");
-    pl.wide = W > kMaxGenericW;
+  } else if (path.rows >= (int64_t(1) << 31) || cdiv(D, 64) > 65535) {
+    return fail(CCV1D_ERR_UNSUPPORTED, "shape too large for the generic kernel");
   }
-  r.Pn = (int32_t)rows;
-  pl.need = partial_bytes(rows, W, D);
-  if (pl.wide) {
-    pl.g_off = g_buffer_offset(pl.need);
-    pl.need = pl.g_off + g_buffer_bytes(B, T, D);
-  }
+  r.Pn = (int32_t)path.rows;
+  pl.g_off = path.g_off;
+  pl.need = path.need;
   return CCV1D_OK;
 }
 
@@ -800,6 +830,19 @@ int run_bwd(BwdPlan& pl, void* workspace, int device, void* stream, bool timed) 
 }  // namespace
 
 extern "C" {
+
+size_t ccv1d_bwd_workspace_bytes_for(const void* x, int64_t x_stride_b, int64_t x_stride_t,
+                                     int x_dtype, const int32_t* seq_idx, const void* dout,
+                                     int64_t dout_stride_b, int64_t dout_stride_t,
+                                     const void* dfinal_states, const void* dx, int64_t batch,
+                                     int64_t seqlen, int64_t dim, int64_t width) {
+  const int64_t B = batch, T = seqlen, D = dim, W = width;
+  if (B <= 0 || T <= 0 || D <= 0 || W < 2 || !valid_dt(x_dtype)) return 0;
+  if (x_stride_b < 0 || x_stride_t < 0 || dout_stride_b < 0 || dout_stride_t < 0) return 0;
+  return bwd_path(x, x_stride_b, x_stride_t, x_dtype, seq_idx != nullptr, dout, dout_stride_b,
+                  dout_stride_t, dfinal_states, dx, T * D, D, true, B, T, D, W)
+      .need;
+}
 
 int ccv1d_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
               const void* weight, int weight_dtype, const void* bias, int bias_dtype,

@@ -217,15 +217,18 @@ struct RowBuf {
     lane_off = (uint32_t)c0 * (uint32_t)sizeof(TX);
     row_bytes = (uint32_t)stride_t * (uint32_t)sizeof(TX);
   }
+  // A row with the buffer's load policy, or with POL for rows that are read again soon (see
+  // bwd_tile's halo).
+  template <int POL = LD>
   __device__ __forceinline__ raw ld(int row) const {
     if constexpr (IO::BYTES == 16)
-      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, (uint32_t)row * row_bytes, LD));
+      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, (uint32_t)row * row_bytes, POL));
     else if constexpr (IO::BYTES == 8)
-      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b64(rs, lane_off, (uint32_t)row * row_bytes, LD));
+      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b64(rs, lane_off, (uint32_t)row * row_bytes, POL));
     else if constexpr (IO::BYTES == 4)
-      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b32(rs, lane_off, (uint32_t)row * row_bytes, LD));
+      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b32(rs, lane_off, (uint32_t)row * row_bytes, POL));
     else
-      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b16(rs, lane_off, (uint32_t)row * row_bytes, LD));
+      return __builtin_bit_cast(raw, __builtin_amdgcn_raw_buffer_load_b16(rs, lane_off, (uint32_t)row * row_bytes, POL));
   }
   __device__ __forceinline__ void st(int row, raw v) const {
     if constexpr (IO::BYTES == 16) {

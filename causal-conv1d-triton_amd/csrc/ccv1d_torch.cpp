@@ -242,6 +242,12 @@ PyObject* bwd_impl(PyObject* const* a) {
   if (dy.get_device() != dev) return assertion("the gradient of out must be on the device of x");
   if (pf && pf->get_device() != dev)
     return assertion("the gradient of final_states must be on the device of x");
+  // The library reads batch * seqlen * dim elements of dout and batch * (width - 1) * dim of
+  // dfinal_states: a smaller tensor would be read past its end.
+  if (dy.sizes() != x.sizes()) return assertion("the gradient of out must have the shape of x");
+  if (pf && (pf->dim() != 3 || pf->size(0) != x.size(0) || pf->size(1) != w.size(1) - 1 ||
+             pf->size(2) != x.size(2)))
+    return assertion("the gradient of final_states must be (batch, width - 1, dim)");
   if (dy.scalar_type() != x.scalar_type() || (pf && pf->scalar_type() != x.scalar_type())) {
     PyErr_SetString(PyExc_TypeError, "the gradients of out and final_states must have x's dtype");
     return nullptr;
@@ -258,7 +264,11 @@ PyObject* bwd_impl(PyObject* const* a) {
   at::Tensor dw = at::empty_like(w);
   at::Tensor db = pb ? at::empty_like(*pb) : at::Tensor();
   at::Tensor di = need_dinit && pi ? at::empty_like(*pi) : at::Tensor();
-  const size_t ws_bytes = ccv1d_bwd_workspace_bytes(B, T, D, W, xdt);
+  // The workspace of the path this call takes (dx is contiguous and the allocation aligned).
+  const size_t ws_bytes = ccv1d_bwd_workspace_bytes_for(
+      x.data_ptr(), x.stride(0), x.stride(1), xdt,
+      ps ? static_cast<const int32_t*>(ps->data_ptr()) : nullptr, dy.data_ptr(), dy.stride(0),
+      dy.stride(1), pf ? pf->data_ptr() : nullptr, dx.data_ptr(), B, T, D, W);
   at::Tensor ws = ws_bytes ? at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte))
                            : at::Tensor();
   void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev)).stream();

@@ -119,6 +119,19 @@ int ccv1d_fwd_inference(const void* x, int64_t x_stride_b, int64_t x_stride_t, i
 size_t ccv1d_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t dim, int64_t width,
                                  int x_dtype);
 
+/* Bytes of device workspace ccv1d_bwd needs for these very tensors: the path its planner picks for
+ * the alignment of x, dout, dfinal_states (may be NULL) and a contiguous dx (batch, seqlen, dim),
+ * and a workspace aligned to 16 bytes (every torch allocation is). Never more than
+ * ccv1d_bwd_workspace_bytes(batch, seqlen, dim, width, x_dtype), and often much less: that bound
+ * covers the generic kernels' tiling (one partial row per 64 rows), which aligned rows never take.
+ * Like the reference's partials allocation (causal_conv1d.py:493), sized from the launch it serves.
+ * 0 for empty or invalid shapes. */
+size_t ccv1d_bwd_workspace_bytes_for(const void* x, int64_t x_stride_b, int64_t x_stride_t,
+                                     int x_dtype, const int32_t* seq_idx, const void* dout,
+                                     int64_t dout_stride_b, int64_t dout_stride_t,
+                                     const void* dfinal_states, const void* dx, int64_t batch,
+                                     int64_t seqlen, int64_t dim, int64_t width);
+
 /* Backward pass. Replaces the host launcher `_bwd` of the reference (causal_conv1d.py:475-541)
  * together with `_bwd_kernel` (causal_conv1d.py:167-341), `_reduce_partials_kernel`
  * (causal_conv1d.py:344-374) and the empty-input path (causal_conv1d.py:480-489).

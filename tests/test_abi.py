@@ -27,7 +27,8 @@ def _declared():
 
 def test_header_declares_the_entry_points():
     assert _declared() == ["ccv1d_abi_version", "ccv1d_bwd", "ccv1d_bwd_dx_strided",
-                           "ccv1d_bwd_noalloc", "ccv1d_bwd_workspace_bytes", "ccv1d_fwd",
+                           "ccv1d_bwd_noalloc", "ccv1d_bwd_workspace_bytes",
+                           "ccv1d_bwd_workspace_bytes_for", "ccv1d_fwd",
                            "ccv1d_fwd_inference", "ccv1d_last_error", "ccv1d_time_main_kernel"]
 
 
@@ -63,6 +64,44 @@ def test_workspace_bytes_of_wide_widths():
         part = B * -(-T // 64) * (W + 1) * D * 4
         want = (part + 255) // 256 * 256 + B * T * D * 4
         assert lib.ccv1d_bwd_workspace_bytes(B, T, D, W, 2) == want
+
+
+def _ws_for(lib, x=1 << 20, sxb=None, sxt=None, xdt=2, seq=None, dy=1 << 24, dfin=None,
+            dx=1 << 28, B=4, T=8192, D=1024, W=4):
+    sxt = D if sxt is None else sxt
+    sxb = T * sxt if sxb is None else sxb
+    return lib.ccv1d_bwd_workspace_bytes_for(x, sxb, sxt, xdt, seq, dy, sxb, sxt, dfin, dx, B, T, D,
+                                             W)
+
+
+def test_workspace_bytes_for_the_call():
+    """The workspace of the path a call takes (its pointers' alignment and strides decide it): the
+    vectorised backward's partial rows for aligned rows, the generic kernels' bound otherwise; never
+    more than the shape-only upper bound. No pointer is dereferenced."""
+    lib = _ffi.load()
+    bound = lib.ccv1d_bwd_workspace_bytes(4, 8192, 1024, 4, 2)
+    fast = _ws_for(lib)
+    # the benchmark shape: 4 batch rows x 32 workgroups along time, (W + 1) x dim fp32 each
+    assert fast == 4 * 32 * 5 * 1024 * 4
+    assert fast < bound
+    # x misaligned by one element: the generic kernels, one partial row per 64-row tile
+    assert _ws_for(lib, x=(1 << 20) + 2) == 4 * (8192 // 64) * 5 * 1024 * 4 <= bound
+    # a time stride that is not a multiple of the channel vector: generic as well
+    assert _ws_for(lib, sxt=1027, sxb=8192 * 1027) == 4 * 128 * 5 * 1024 * 4
+    # width above 128: partial rows plus the fp32 g buffer, as the shape-only bound says
+    assert _ws_for(lib, B=2, T=300, D=100, W=129) == lib.ccv1d_bwd_workspace_bytes(2, 300, 100, 129, 2)
+    # empty and invalid shapes
+    assert _ws_for(lib, B=0) == 0 and _ws_for(lib, T=0) == 0 and _ws_for(lib, W=1) == 0
+    assert _ws_for(lib, xdt=9) == 0
+    # random shapes: never above the bound
+    import random
+    rnd = random.Random(0)
+    for _ in range(200):
+        B, T, D, W = rnd.randint(1, 8), rnd.randint(1, 5000), rnd.randint(1, 3000), rnd.randint(2, 40)
+        xdt = rnd.choice([0, 1, 2, 3])
+        n = _ws_for(lib, B=B, T=T, D=D, W=W, xdt=xdt, x=(1 << 20) + rnd.choice([0, 2, 16]),
+                    seq=rnd.choice([None, 1 << 30]))
+        assert 0 < n <= lib.ccv1d_bwd_workspace_bytes(B, T, D, W, xdt), (B, T, D, W, xdt)
 
 
 def _fwd(lib, **kw):

@@ -149,3 +149,34 @@ def test_host_gradients_rejected_before_launch(which):
             dfin = torch.randn(B, W - 1, D).to(torch.bfloat16)
         with pytest.raises(AssertionError, match="device of x"):
             _bwd(x, w, None, None, None, dout, dfin, False, True)
+
+
+@pytest.mark.parametrize("which,shape", [
+    ("dout", (2, 15, 8)), ("dfinal_states", (3, 8)), ("dfinal_states", (2, 3, 7)),
+    ("dfinal_states", (2, 2, 8)),
+])
+def test_misshaped_gradients_rejected_before_launch(which, shape):
+    """The backward entries refuse incoming gradients smaller (or otherwise shaped) than out and the
+    final states: the library would read batch * seqlen * dim and batch * (width - 1) * dim
+    elements from them. Checked before any launch, in causal_conv1d_bwd (fused.py) and in the
+    autograd node's backward."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from causal_conv1d_triton.causal_conv1d import _bwd
+    from causal_conv1d_triton.fused import causal_conv1d_bwd
+
+    B, T, D, W = 2, 16, 8, 4
+    with FakeTensorMode():
+        x = torch.empty(B, T, D, device="cuda", dtype=torch.bfloat16)
+        w = torch.empty(D, W, device="cuda")
+        dout = torch.empty(B, T, D, device="cuda", dtype=torch.bfloat16)
+        dfin = torch.empty(B, W - 1, D, device="cuda", dtype=torch.bfloat16)
+        bad = torch.empty(shape, device="cuda", dtype=torch.bfloat16)
+        if which == "dout":
+            dout = bad
+        else:
+            dfin = bad
+        with pytest.raises(AssertionError, match="shape|width - 1"):
+            causal_conv1d_bwd(x, w, None, dout, dfinal_states=dfin, activation="silu")
+        with pytest.raises(AssertionError, match="shape|width - 1"):
+            _bwd(x, w, None, None, None, dout, dfin, False, True)
