@@ -1045,6 +1045,7 @@ def _direct_bwd_call(x, w, b, dy, ws, silu=True, stream=None):
 
 @pytest.mark.parametrize("B,T,D,W,bias", [
     (4, 2048, 1024, 4, True),
+    (4, 8192, 1024, 4, True),    # 128 partial rows per wave column: the reduction kernel
     (2, 4096, 2048, 4, False),   # no bias: W value rows per channel
     (3, 777, 1000, 3, True),     # last wave column partly outside dim (1000 = 3 * 256 + 232)
     (1, 17, 256, 8, True),       # one partial row per wave column
@@ -1073,6 +1074,49 @@ def test_dweight_repeatable_with_garbage_workspace(B, T, D, W, bias):
     check_sum(results[0][0], ref["dw"], "dweight")
     if bias:
         check_sum(results[0][1], ref["db"], "dbias")
+
+
+@pytest.mark.parametrize("B,T,D,W,bias", [
+    (4, 512, 1024, 4, True),     # 32 partial rows per wave column (fewer than the 16 row sets x 8)
+    (4, 2048, 1024, 4, True),
+    (3, 777, 1000, 3, True),     # a wave column partly outside dim
+    (2, 300, 96, 7, False),      # no bias, 2 channels per lane
+    (1, 17, 256, 8, True),       # one partial row
+    (4, 8192, 1024, 4, True),    # 128 rows
+    (2, 8192, 2048, 4, False),
+])
+def test_reduction_order_matches_partial_rows(B, T, D, W, bias):
+    """dweight/dbias equal, bit for bit, the fp32 sums of the partial rows the backward leaves at
+    the start of its workspace ((rows, W + 1, dim) floats), added in the order reduce_partials_kernel
+    documents: 16 interleaved row sets (set j holds rows j, j + 16, ...) each summed in row order
+    from zero, then the set sums added in set order. A row missed or read before its writer
+    finished would change the bits."""
+    from causal_conv1d_triton import _ffi
+
+    inp = make_inputs(90 + W, B, T, D, W, bias=bias)
+    x, w, dy = inp["x"].to(DEV), inp["w"].to(DEV), inp["dy"].to(DEV)
+    b = inp["b"].to(DEV) if bias else None
+    n = _ffi.bwd_workspace_bytes(B, T, D, W, torch.bfloat16)
+    ws = torch.randint(0, 256, (n,), dtype=torch.uint8, device=DEV,
+                       generator=torch.Generator(device=DEV).manual_seed(3))
+    _, dw, db = _direct_bwd_call(x, w, b, dy, ws)
+    torch.cuda.synchronize()
+    rows = _ffi.bwd_workspace_bytes_for(x, None, dy, None, torch.empty_like(x), W)
+    rows //= (W + 1) * D * 4
+    part = ws[:rows * (W + 1) * D * 4].view(torch.float32).view(rows, W + 1, D).cpu()
+    sets = []
+    for j in range(16):
+        a = torch.zeros(W + 1, D)
+        for r in range(j, rows, 16):
+            a = a + part[r]
+        sets.append(a)
+    acc = sets[0]
+    for a in sets[1:]:
+        acc = acc + a
+    assert torch.equal(dw.cpu(), acc[:W].t().contiguous())
+    if bias:
+        assert torch.equal(db.cpu(), acc[W])
+    check_sum(dw.cpu(), oracle_ref(inp, True)["dw"], "dweight")
 
 
 def test_back_to_back_calls_share_one_workspace():
@@ -1123,7 +1167,8 @@ def test_concurrent_streams():
             assert torch.equal(u, v)
 
 
-@pytest.mark.parametrize("B,T,D,W", [(2, 4096, 1024, 4), (2, 700, 96, 64), (2, 700, 96, 128)])
+@pytest.mark.parametrize("B,T,D,W", [(2, 4096, 1024, 4), (4, 512, 1024, 4), (2, 700, 96, 64),
+                                     (2, 700, 96, 128)])
 def test_graph_replays_match_eager(B, T, D, W):
     """fwd+bwd captured in a HIP graph and replayed several times, with the program's own eager work
     and synchronisations in between; every replay must equal the eager result bit for bit. Widths
