@@ -391,6 +391,17 @@ bool aligned_to(const void* p, int64_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)bytes) == 0;
 }
 
+// A channel slice of a wider channels-last tensor (strides other than the contiguous (T * D, D))
+// whose rows do not all start on a 128-byte line: each row's first and last lines, and the lines
+// where neighbouring wave columns meet, are shared with other columns (TileCoord's col_fast).
+bool straddling_slice(const void* p, int64_t s_b, int64_t s_t, int64_t B, int64_t T, int64_t D,
+                      int es) {
+  if ((s_t == D || T == 1) && (s_b == T * D || B == 1)) return false;
+  const bool aligned = aligned_to(p, 128) && (T == 1 || (s_t * es) % 128 == 0) &&
+                       (B == 1 || (s_b * es) % 128 == 0);
+  return !aligned;
+}
+
 uint32_t slab_bytes(int x_dt, int64_t T, int64_t D, int64_t s_t) {
   return (uint32_t)(((T - 1) * s_t + D) * esize(x_dt));
 }
@@ -469,6 +480,7 @@ int fwd_entry(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   if (T > 0) {
     if (fast) {
       tl = fwd_fast_tiling(B, T, D, W, x_dtype, seq_idx != nullptr);
+      tl.col_fast = straddling_slice(x, x_stride_b, x_stride_t, B, T, D, esize(x_dtype));
     } else {
       tl = generic_tiling(T);
       if (B * tl.nT >= (int64_t(1) << 31) || cdiv(D, 64) > 65535)
@@ -763,6 +775,11 @@ int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
     p.x_bytes = slab_bytes(x_dtype, T, D, x_stride_t);
     p.y_bytes = slab_bytes(x_dtype, T, D, dout_stride_t);
     p.o_bytes = slab_bytes(x_dtype, T, D, dx_stride_t);
+    const int es = esize(x_dtype);
+    const bool dx_straddles = straddling_slice(dx, dx_stride_b, dx_stride_t, B, T, D, es);
+    p.tl.col_fast = dx_straddles || straddling_slice(x, x_stride_b, x_stride_t, B, T, D, es) ||
+                    straddling_slice(dout, dout_stride_b, dout_stride_t, B, T, D, es);
+    p.dx_nt = dx_straddles;
   } else if (path.rows >= (int64_t(1) << 31) || cdiv(D, 64) > 65535) {
     return fail(CCV1D_ERR_UNSUPPORTED, "shape too large for the generic kernel");
   }

@@ -22,6 +22,10 @@ struct Tiling {
   int32_t nTB;   // workgroups along time per batch row: ceil(nT / NW)
   int32_t nBlk;  // workgroups in the grid: B * nGW * nTB
   int32_t vec;   // channels per lane the tiling was made for (0 for the generic kernels)
+  // Workgroup order: 0 = time fastest (a wave column's consecutive time tiles are consecutive
+  // workgroups), 1 = wave column fastest (the columns of one range of rows are), for rows that are
+  // not aligned to the 128-byte line, whose lines straddle neighbouring columns (TileCoord).
+  int32_t col_fast;
 };
 
 struct FwdParams {
@@ -59,6 +63,7 @@ struct BwdParams {
   int32_t w_dt, b_dt, i_dt;
   int32_t has_bias, has_init, has_dfinal, need_dinit, silu;
   uint32_t x_bytes, y_bytes, o_bytes;  // per-batch byte extents of x, dout and dx (vectorised)
+  int32_t dx_nt;  // host side: dx rows straddle 128-byte lines, stored non-temporally (BwdCfg)
   Tiling tl;
 };
 

@@ -95,6 +95,15 @@ __device__ __forceinline__ void shift_in(int32_t (&win)[P], int32_t v) {
 // half the channels. Measured on MI355X: at B=4 T=8192 D=4096 the step takes 246 us with chunks
 // of 512 against 334 us with one remap over the grid; grids of at most 512 workgroups (the
 // B=4 T=8192 D=1024 benchmark) are mapped as before.
+//
+// With Tiling::col_fast the wave columns of one range of rows are consecutive instead: where rows
+// are not aligned to the 128-byte line (x a channel slice of a wider tensor, dx written into one),
+// the lines at the column boundaries are shared by two columns, and with this order both columns
+// touch them on the same XCD at about the same time. Measured at Mamba-2's in_proj slice (B=8
+// T=4096 D=5376, row pitch 10576 channels, configuration 3): fwd+bwd 327 -> 320 us, backward with
+// dx written into the in_proj gradient 256 -> 247 us (233 with non-temporal dx stores, see
+// BwdCfg); on aligned rows the time-fastest order is faster (benchmark step 59.7 against 62.6 us,
+// 11 of 13 mid-size shapes).
 constexpr int kXcdChunk = 512;
 struct TileCoord {
   int b, gw, tb;
@@ -102,10 +111,17 @@ struct TileCoord {
     const int chunk = blockIdx.x / kXcdChunk;
     const int first = chunk * kXcdChunk;
     const int blk = first + xcd_remap(blockIdx.x - first, min(kXcdChunk, tl.nBlk - first));
-    tb = blk % tl.nTB;
-    const int rest = blk / tl.nTB;
-    gw = rest % tl.nGW;
-    b = rest / tl.nGW;
+    if (tl.col_fast) {
+      gw = blk % tl.nGW;
+      const int rest = blk / tl.nGW;
+      tb = rest % tl.nTB;
+      b = rest / tl.nTB;
+    } else {
+      tb = blk % tl.nTB;
+      const int rest = blk / tl.nTB;
+      gw = rest % tl.nGW;
+      b = rest / tl.nGW;
+    }
   }
 };
 

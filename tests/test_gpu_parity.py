@@ -1211,7 +1211,7 @@ def test_graph_replays_match_eager(B, T, D, W):
 # ------------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("case", ["aligned", "odd_offset", "generic_width", "wide_width", "seq_idx",
-                                  "states"])
+                                  "states", "straddling"])
 def test_backward_into_strided_dx(case):
     """causal_conv1d_bwd writes dx into channels [c0, c0 + dim) of a wider buffer: the same bits
     as the contiguous backward, and every other element of the buffer untouched. At an odd channel
@@ -1223,6 +1223,10 @@ def test_backward_into_strided_dx(case):
     B, T, D, W, c0, wide = 2, 700, 512, 4, 512, 1536
     if case == "odd_offset":
         c0 = 3                       # rows misaligned for the vectorised kernels: generic path
+    if case == "straddling":
+        # a 3104-byte pitch: rows start 0, 32, 64 or 96 bytes into a 128-byte line, so the
+        # backward takes the column-fastest workgroup order and non-temporal dx stores
+        wide = 1552
     if case == "generic_width":
         W = 20
     if case == "wide_width":
@@ -1259,3 +1263,30 @@ def test_backward_into_strided_dx(case):
     ref = oracle_ref(inp, True, dfinal=dfin is not None, need_dinit=init)
     check_lowp(dx.cpu(), ref["dx"], False, "dx")
     check_sum(dw.cpu(), ref["dw"], "dweight")
+
+
+@pytest.mark.parametrize("W", [4, 7])
+def test_straddling_slices_match_contiguous(W):
+    """x and the upstream gradient as channel slices of wider tensors whose rows straddle 128-byte
+    lines (a pitch of 1552 channels, like Mamba-2's in_proj output) take the column-fastest
+    workgroup order in both passes; every result is bit-identical to the same call on contiguous
+    copies."""
+    B, T, D, c0, wide = 2, 600, 512, 512, 1552
+    inp = make_inputs(44, B, T, D, W, init=True)
+    x, w, b, dy, s0 = (inp[k].to(DEV) for k in ("x", "w", "b", "dy", "init"))
+
+    def run(xv, dyv):
+        xv = xv.detach().requires_grad_(True)
+        wv, bv, sv = (t.clone().requires_grad_(True) for t in (w, b, s0))
+        out = causal_conv1d_fn(xv, wv, bv, initial_states=sv, activation="silu")
+        grads = torch.autograd.grad(out, (xv, wv, bv, sv), dyv)
+        return (out,) + grads
+
+    bx = torch.zeros(B, T, wide, dtype=x.dtype, device=DEV)
+    by = torch.zeros(B, T, wide, dtype=x.dtype, device=DEV)
+    bx[..., c0:c0 + D] = x
+    by[..., c0:c0 + D] = dy
+    got = run(bx[..., c0:c0 + D], by[..., c0:c0 + D])
+    want = run(x, dy)
+    for g, e in zip(got, want):
+        assert torch.equal(g, e)
