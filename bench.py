@@ -63,6 +63,9 @@ def _capture(fn, warm_stream):
     return g
 
 
+# Calls per captured graph of the --configs, --widths and --shapes measurements.
+CONFIG_GRAPH_CALLS = 32
+
 # Steps per captured graph of the headline measurement (main()).
 GRAPH_STEPS = 64
 
@@ -332,35 +335,46 @@ def run_configs(dev, widths=False, only=None, shapes=False):
             line.update(extra)
         print(json.dumps(line), flush=True)
 
-    def timed(graph, per_replay):
+    def timed(graph_calls):
+        # graph_calls: (graph, calls per replay); device time per call in us
+        graph, per_replay = graph_calls
         _warm(graph, 2)
         reps = 20
         return _time_graphs([graph] * reps) / (reps * per_replay) * 1e3
 
+    def looped(one_pass, n):
+        # One graph that runs one_pass (n calls over the input sets) enough times to hold about
+        # CONFIG_GRAPH_CALLS calls, so the idle gap between two graph replays (the next graph's
+        # launch, about 3.6 us) weighs little on the time per call. Returns (graph, calls).
+        rounds = max(1, CONFIG_GRAPH_CALLS // n)
+        return _capture(lambda: [one_pass() for _ in range(rounds)], side), rounds * n
+
     def steps(sets, w, b, act, init=None, seq=None, xs=None):
         res = []
 
-        def fn():
+        def one_pass():
             for i, (x, dy) in enumerate(sets):
                 xi = x if xs is None else xs[i]
                 out = causal_conv1d_fn(xi, w, b, seq_idx=seq, initial_states=init, activation=act)
                 grads = [t for t in (xi, w, b, init) if t is not None and t.requires_grad]
                 res.append(torch.autograd.grad(out, grads, dy))
-        g = _capture(fn, side)
+                del res[:-len(sets)]  # the last pass's gradients stay allocated
+        gc = looped(one_pass, len(sets))
         res.clear()
-        return g
+        return gc
 
     def fwds(sets, w, b, act):
         # Forward alone, as inference calls it: causal_conv1d_fn with autograd off.
         res = []
 
-        def fn():
+        def one_pass():
             with torch.no_grad():
                 for x, _ in sets:
                     res.append(causal_conv1d_fn(x, w, b, activation=act))
-        g = _capture(fn, side)
+                    del res[:-len(sets)]
+        gc = looped(one_pass, len(sets))
         res.clear()
-        return g
+        return gc
 
     if widths:
         B, T, D = 4, 8192, 1024
@@ -375,8 +389,8 @@ def run_configs(dev, widths=False, only=None, shapes=False):
             w = (torch.randn(D, W, generator=gen, device=dev) / math.sqrt(W)).requires_grad_(True)
             fb, bb = _alg_bytes_general(B, T, D, W, True)
             shape = f"B={B} T={T} D={D} W={W} bias_silu"
-            emit("widths", shape, timed(fwds(sets, w, b, "silu"), len(sets)), fb, bb, "fwd")
-            emit("widths", shape, timed(steps(sets, w, b, "silu"), len(sets)), fb, bb, "fwd+bwd")
+            emit("widths", shape, timed(fwds(sets, w, b, "silu")), fb, bb, "fwd")
+            emit("widths", shape, timed(steps(sets, w, b, "silu")), fb, bb, "fwd+bwd")
         return
 
     if shapes:
@@ -396,8 +410,8 @@ def run_configs(dev, widths=False, only=None, shapes=False):
                 w = (torch.randn(D, W, generator=gen, device=dev) / math.sqrt(W)).requires_grad_(True)
                 fb, bb = _alg_bytes_general(B, T, D, W, True)
                 shape = f"B={B} T={T} D={D} W={W} bias_silu"
-                emit("shapes", shape, timed(fwds(sets, w, b, "silu"), nsets), fb, bb, "fwd")
-                emit("shapes", shape, timed(steps(sets, w, b, "silu"), nsets), fb, bb, "fwd+bwd")
+                emit("shapes", shape, timed(fwds(sets, w, b, "silu")), fb, bb, "fwd")
+                emit("shapes", shape, timed(steps(sets, w, b, "silu")), fb, bb, "fwd+bwd")
             del sets
         return
 
@@ -422,19 +436,19 @@ def run_configs(dev, widths=False, only=None, shapes=False):
             # forward alone over at least 512 MiB of x, twice the Infinity Cache
             fsets = sets + [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16),
                              None) for _ in range(max(0, nfwd - nsets))]
-            emit("2", shape, timed(fwds(fsets, w, b, act), len(fsets)), fb, bb, "fwd")
+            emit("2", shape, timed(fwds(fsets, w, b, act)), fb, bb, "fwd")
             del fsets
-            emit("2", shape, timed(steps(sets, w, b, act), nsets), fb, bb, "fwd+bwd")
+            emit("2", shape, timed(steps(sets, w, b, act)), fb, bb, "fwd+bwd")
         del sets
     if want(3):
-        run_config3(dev, gen, emit, timed, steps)
+        run_config3(dev, gen, emit, timed, steps, looped)
     if want(4):
         run_config4(dev, gen, emit, timed, side)
     if any(want(5, W) for W in (4, 7)):
         run_config5(dev, gen, emit, timed, steps, [W for W in (4, 7) if want(5, W)])
 
 
-def run_config3(dev, gen, emit, timed, steps):
+def run_config3(dev, gen, emit, timed, steps, looped):
     """Configuration 3: Mamba-2 2.7B xBC, x a channel slice of an in_proj output."""
     B, T, D, W = 8, 4096, 5376, 4
     bigs = [torch.randn(B, T, 10576, generator=gen, device=dev).to(torch.bfloat16) for _ in range(2)]
@@ -444,7 +458,7 @@ def run_config3(dev, gen, emit, timed, steps):
     b = ((torch.rand(D, generator=gen, device=dev) - 0.5) * 0.2).requires_grad_(True)
     fb, bb = _alg_bytes_general(B, T, D, W, True)
     emit("3", f"B={B} T={T} D={D} W={W} x=slice(in_proj, stride 10576)",
-         timed(steps(sets, w, b, "silu", xs=xs), 2), fb, bb, "fwd+bwd")
+         timed(steps(sets, w, b, "silu", xs=xs)), fb, bb, "fwd+bwd")
     # The backward's dx into the gradient of the in_proj output: written in place through the
     # strided-dx entry point, against a contiguous dx copied into its slice afterwards (what
     # assembling that gradient from the slices' gradients costs).
@@ -463,13 +477,12 @@ def run_config3(dev, gen, emit, timed, steps):
         for (x, dy), gz in zip(sets, grads):
             causal_conv1d_bwd(x.detach(), wd, bd, dy, dx=gz[..., 5120:5120 + D], activation="silu")
 
-    side = torch.cuda.Stream()
     saved = 2 * B * T * D * 2
     emit("3", f"B={B} T={T} D={D} W={W} backward, dx copied into the in_proj gradient", 
-         timed(_capture(copied, side), 2), 0, bb + saved, "bwd",
+         timed(looped(copied, 2)), 0, bb + saved, "bwd",
          {"alg_bytes": bb + saved})
     emit("3", f"B={B} T={T} D={D} W={W} backward, dx written into the in_proj gradient",
-         timed(_capture(in_place, side), 2), 0, bb, "bwd",
+         timed(looped(in_place, 2)), 0, bb, "bwd",
          {"alg_bytes": bb, "bytes_saved_per_step": saved})
     del grads
 
@@ -480,7 +493,7 @@ def run_config3(dev, gen, emit, timed, steps):
         for x, dy in sets:
             _bwd(x.detach(), wd, bd, None, None, dy, None, False, True)
 
-    emit("3", f"B={B} T={T} D={D} W={W} backward, contiguous dx", timed(_capture(contiguous, side), 2),
+    emit("3", f"B={B} T={T} D={D} W={W} backward, contiguous dx", timed(looped(contiguous, 2)),
          0, bb, "bwd", {"alg_bytes": bb})
     padded = [torch.empty(B, T, 10624, dtype=torch.bfloat16, device=dev) for _ in range(2)]
 
@@ -489,7 +502,7 @@ def run_config3(dev, gen, emit, timed, steps):
             causal_conv1d_bwd(x.detach(), wd, bd, dy, dx=gz[..., 5120:5120 + D], activation="silu")
 
     emit("3", f"B={B} T={T} D={D} W={W} backward, dx written into a gradient of 10624 channels",
-         timed(_capture(in_place_padded, side), 2), 0, bb, "bwd", {"alg_bytes": bb})
+         timed(looped(in_place_padded, 2)), 0, bb, "bwd", {"alg_bytes": bb})
     del bigs, xs, sets, padded
 
 
@@ -511,7 +524,7 @@ def run_config4(dev, gen, emit, timed, side):
                                             activation="silu")
         with torch.no_grad():
             g = _capture(stream_fn, side)
-            dev_us = timed(g, n)
+            dev_us = timed((g, n))
             for _ in range(3):
                 stream_fn()
             torch.cuda.synchronize()
@@ -552,7 +565,7 @@ def run_config5(dev, gen, emit, timed, steps, widths):
         init.requires_grad_(True)
         fb, bb = _alg_bytes_general(B, T, D, W, True, init=True, seq=True)
         emit("5", f"B={B} T={T} D={D} W={W} seq_idx varlen, initial_states",
-             timed(steps(sets, w, b, "silu", init=init, seq=seq), 2), fb, bb, "fwd+bwd")
+             timed(steps(sets, w, b, "silu", init=init, seq=seq)), fb, bb, "fwd+bwd")
         del sets
 
 
