@@ -480,7 +480,8 @@ int fwd_entry(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype
   if (T > 0) {
     if (fast) {
       tl = fwd_fast_tiling(B, T, D, W, x_dtype, seq_idx != nullptr);
-      tl.col_fast = straddling_slice(x, x_stride_b, x_stride_t, B, T, D, esize(x_dtype));
+      tl.col_fast = W <= kColFastMaxW &&
+                    straddling_slice(x, x_stride_b, x_stride_t, B, T, D, esize(x_dtype));
     } else {
       tl = generic_tiling(T);
       if (B * tl.nT >= (int64_t(1) << 31) || cdiv(D, 64) > 65535)
@@ -777,8 +778,9 @@ int plan_bwd(const void* x, int64_t x_stride_b, int64_t x_stride_t, int x_dtype,
     p.o_bytes = slab_bytes(x_dtype, T, D, dx_stride_t);
     const int es = esize(x_dtype);
     const bool dx_straddles = straddling_slice(dx, dx_stride_b, dx_stride_t, B, T, D, es);
-    p.tl.col_fast = dx_straddles || straddling_slice(x, x_stride_b, x_stride_t, B, T, D, es) ||
-                    straddling_slice(dout, dout_stride_b, dout_stride_t, B, T, D, es);
+    p.tl.col_fast = W <= kColFastMaxW &&
+                    (dx_straddles || straddling_slice(x, x_stride_b, x_stride_t, B, T, D, es) ||
+                     straddling_slice(dout, dout_stride_b, dout_stride_t, B, T, D, es));
     p.dx_nt = dx_straddles;
   } else if (path.rows >= (int64_t(1) << 31) || cdiv(D, 64) > 65535) {
     return fail(CCV1D_ERR_UNSUPPORTED, "shape too large for the generic kernel");

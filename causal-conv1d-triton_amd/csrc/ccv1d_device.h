@@ -27,6 +27,8 @@ struct Tiling {
   // not aligned to the 128-byte line, whose lines straddle neighbouring columns (TileCoord).
   int32_t col_fast;
 };
+// Widest kernels that follow Tiling::col_fast (wider ones always run time fastest).
+constexpr int kColFastMaxW = 8;
 
 struct FwdParams {
   const void* x;
@@ -63,8 +65,10 @@ struct BwdParams {
   int32_t w_dt, b_dt, i_dt;
   int32_t has_bias, has_init, has_dfinal, need_dinit, silu;
   uint32_t x_bytes, y_bytes, o_bytes;  // per-batch byte extents of x, dout and dx (vectorised)
-  int32_t dx_nt;  // host side: dx rows straddle 128-byte lines, stored non-temporally (BwdCfg)
   Tiling tl;
+  // Host side: dx rows straddle 128-byte lines, stored non-temporally (BwdCfg). Kept after tl: in
+  // front of it the widest kernels' kernel-argument loads left them 20-400 more SGPR spills.
+  int32_t dx_nt;
 };
 
 struct ReduceParams {

@@ -104,14 +104,18 @@ __device__ __forceinline__ void shift_in(int32_t (&win)[P], int32_t v) {
 // dx written into the in_proj gradient 256 -> 247 us (233 with non-temporal dx stores, see
 // BwdCfg); on aligned rows the time-fastest order is faster (benchmark step 59.7 against 62.6 us,
 // 11 of 13 mid-size shapes).
+// Kernels of widths above kColFastMaxW (COL_FAST false) always take the time-fastest order: the
+// branch cost the widest backward kernels up to 400 SGPR spills (W=32 step +4 us), and the slices
+// it serves are measured at width 4.
 constexpr int kXcdChunk = 512;
+template <bool COL_FAST>
 struct TileCoord {
   int b, gw, tb;
   __device__ __forceinline__ TileCoord(const Tiling& tl) {
     const int chunk = blockIdx.x / kXcdChunk;
     const int first = chunk * kXcdChunk;
     const int blk = first + xcd_remap(blockIdx.x - first, min(kXcdChunk, tl.nBlk - first));
-    if (tl.col_fast) {
+    if (COL_FAST && tl.col_fast) {
       gw = blk % tl.nGW;
       const int rest = blk / tl.nGW;
       tb = rest % tl.nTB;
@@ -396,7 +400,7 @@ __global__ __launch_bounds__(NW * 64, (fwd_waves_per_simd<TX, W, SEQ>())) void f
   constexpr int P = W - 1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const TileCoord tc(p.tl);
+  const TileCoord<(W <= kColFastMaxW)> tc(p.tl);
   const int tile = tc.tb * NW + wave;
   if (tile >= p.tl.nT) return;
   const int T = p.T, D = p.D;
@@ -589,7 +593,7 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const TileCoord tc(p.tl);
+  const TileCoord<(W <= kColFastMaxW)> tc(p.tl);
   const int tile = tc.tb * NW + wave;
   const int G = p.D / CPL;
   const int grp = tc.gw * 64 + lane;
@@ -655,23 +659,25 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
     // requested before anything waits on memory (rows past t_end are clamped to the last row).
     const bool halo_in_x = t0 >= P;
     raw hr[P], px[P], py[P];
+    // Up to width 8 the rows a neighbouring wave reads again are loaded with the plain policy
+    // (x's and dout's other loads are non-temporal, the first to be evicted), so they are still in
+    // the L2 when it comes: the halo rows are also the last P rows of the previous tile, read at
+    // the end of its walk, and the first wave's first P rows are the right halo of the previous
+    // workgroup's last wave. Step B=4 T=8192 D=1024 bf16: W=4 60.6 -> 59.9 us (halo rows) -> 59.75
+    // (first rows; plain first rows in every wave, which no other wave reads: 60.2), W=8 unchanged;
+    // from W=9 the W-1 cached rows per tile cost more than they save (W=9 +0.5 us, W=32 +4 us).
+    constexpr int HALO_LD = W <= 8 ? kCachePlain : XLD;
+    constexpr int FIRST_YLD = W <= 8 ? kCachePlain : YLD;
     if (halo_in_x) {
-      // The halo rows are also the last P rows of the previous tile, which its wave reads at the
-      // end of its walk: loaded with the plain policy (x's other loads are non-temporal, the
-      // first to be evicted), they are still in the L2 then. Step B=4 T=8192 D=1024 W=4 bf16
-      // 60.6 -> 59.9 us.
 #pragma unroll
-      for (int k = 0; k < P; ++k) hr[k] = X.template ld<kCachePlain>(t0 - P + k);
+      for (int k = 0; k < P; ++k) hr[k] = X.template ld<HALO_LD>(t0 - P + k);
     }
-    // The first wave's first P rows are the right halo of the previous workgroup's last wave,
-    // which reads them at the end of its walk: plain policy as well (60.0 -> 59.9 us; for every
-    // wave's first rows, which no other wave reads, 60.2 us).
 #pragma unroll
     for (int q = 0; q < P; ++q) {
       const int row = min(t0 + q, t_end - 1);
-      if (wave == 0) {
-        px[q] = X.template ld<kCachePlain>(row);
-        py[q] = PAD ? raw{} : Y.template ld<kCachePlain>(row);
+      if (W <= 8 && wave == 0) {
+        px[q] = X.template ld<HALO_LD>(row);
+        py[q] = PAD ? raw{} : Y.template ld<FIRST_YLD>(row);
       } else {
         px[q] = X.ld(row);
         py[q] = PAD ? raw{} : Y.ld(row);
@@ -845,7 +851,7 @@ __global__ __launch_bounds__(NW * 64, (bwd_waves_per_simd<TX, W, CPL>())) void b
   __shared__ float lds[bwd_lds_floats<W, CPL, NW>()];
   if constexpr (SEQ) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const TileCoord tc(p.tl);
+    const TileCoord<(W <= kColFastMaxW)> tc(p.tl);
     const int tile = tc.tb * NW + wave;
     const int t0 = tile * p.tl.L;
     const int r1 = min(t0 + p.tl.L + W - 1, p.T);
