@@ -363,14 +363,15 @@ def run_configs(dev, widths=False, only=None, shapes=False):
         res.clear()
         return gc
 
-    def fwds(sets, w, b, act):
-        # Forward alone, as inference calls it: causal_conv1d_fn with autograd off.
+    def fwds(sets, w, b, act, op=None):
+        # Forward alone, as inference calls it: causal_conv1d_fn with autograd off. With `op`
+        # (a one-argument function of x), that function instead, under the same rotation.
         res = []
 
         def one_pass():
             with torch.no_grad():
                 for x, _ in sets:
-                    res.append(causal_conv1d_fn(x, w, b, activation=act))
+                    res.append(causal_conv1d_fn(x, w, b, activation=act) if op is None else op(x))
                     del res[:-len(sets)]
         gc = looped(one_pass, len(sets))
         res.clear()
@@ -437,6 +438,11 @@ def run_configs(dev, widths=False, only=None, shapes=False):
             fsets = sets + [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16),
                              None) for _ in range(max(0, nfwd - nsets))]
             emit("2", shape, timed(fwds(fsets, w, b, act)), fb, bb, "fwd")
+            if bias:
+                # The copy ceiling of the forward alone: torch's clone of the same x under the same
+                # rotation (reads and writes the forward's activation bytes, nothing else).
+                emit("2", f"B={B} T={T} D={D} torch clone of x", timed(fwds(fsets, w, b, act,
+                     op=torch.clone)), 2 * B * T * D * 2, 0, "fwd", {"reference": "copy"})
             del fsets
             emit("2", shape, timed(steps(sets, w, b, act)), fb, bb, "fwd+bwd")
         del sets
