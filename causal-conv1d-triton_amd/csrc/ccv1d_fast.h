@@ -654,7 +654,6 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
   };
 
   float* halo_out = lds + wave * P * COLS + lane * CPL;
-  const bool b_early = t_end - t_main > R && t_end - t_main < 2 * R;
   if (active) {
     // The halo rows, the tile's first P rows, the first pipelined batch and the taps are all
     // requested before anything waits on memory (rows past t_end are clamped to the last row).
@@ -685,10 +684,6 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
       }
     }
     load(Ax, Ay, t_main);
-    if constexpr (CPL * sizeof(TX) <= 4) {
-      // A short tile's rows after the first batch (no pipelined loop follows): requested now too.
-      if (b_early) load(Bx, By, t_main + R);
-    }
     load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
     if (SILU && !PAD) {
       // silu' in the base-2 domain (dsilu_scaled): weights and bias times -log2(e).
@@ -752,43 +747,14 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
       load(Ax, Ay, t + 2 * R);
       compute(Bx, By, t + R);
     }
-    // The last 0 .. 2R-1 rows. A holds rows t .. t+R-1. Where the lanes' rows are at most 4 bytes
-    // (registers to spare), the rows after A are requested before A is computed, or with the
-    // tile's first requests when no loop ran (b_early), so no row waits on a load issued right
-    // before its use: B=4 D=1024 fwd+bwd T=512 12.81 -> 12.62 us, T=2048 21.3 -> 21.1-21.2 (2
-    // channels per lane). With 4 channels the extra batch spilled registers (W=4: 92 bytes per
-    // lane), so those kernels keep one batch and load the last rows one by one.
-    const int rem = t_end - t;
-    auto compute_n = [&](const raw (&bx)[R], const raw (&by)[R], int t, int n) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (r < n) {
-          float dx[CPL];
-          s.step(t + r, bx[r], by[r], SEQ ? ids.at(t + r) : 0, dx);
-          DX.st(t + r - P, IO::pack(dx));
-        }
-      }
-    };
-    if constexpr (CPL * sizeof(TX) <= 4) {
-      if (rem > R) {
-        if (!b_early) load(Bx, By, t + R);
-        compute(Ax, Ay, t);
-        compute_n(Bx, By, t + R, rem - R);
-      } else if (rem == R) {
-        compute(Ax, Ay, t);
-      } else if (rem > 0) {
-        compute_n(Ax, Ay, t, rem);
-      }
-    } else {
-      if (t + R <= t_end) {
-        compute(Ax, Ay, t);
-        t += R;
-      }
-      for (; t < t_end; ++t) {
-        float dx[CPL];
-        s.step(t, X.ld(t), PAD ? raw{} : Y.ld(t), SEQ ? ids.at(t) : 0, dx);
-        emit_any(t - P, dx);
-      }
+    if (t + R <= t_end) {
+      compute(Ax, Ay, t);
+      t += R;
+    }
+    for (; t < t_end; ++t) {
+      float dx[CPL];
+      s.step(t, X.ld(t), PAD ? raw{} : Y.ld(t), SEQ ? ids.at(t) : 0, dx);
+      emit_any(t - P, dx);
     }
 
     if (succ_here) {
