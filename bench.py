@@ -304,7 +304,7 @@ def _alg_bytes_general(B, T, D, W, bias, init=False, seq=False, final=False, ex=
     return fwd, bwd
 
 
-def run_configs(dev, widths=False, only=None, shapes=False):
+def run_configs(dev, widths=False, only=None, shapes=False, x_dtype=torch.bfloat16):
     """One JSON line per BASELINE configuration 2-5 (the reference's README sweep, the Mamba-2 xBC
     shape, chunked streaming and decode with state handoff, packed varlen seq_idx): device time per
     call from replayed graphs after the usual warm-up, plus, for the latency-bound streaming and
@@ -316,7 +316,9 @@ def run_configs(dev, widths=False, only=None, shapes=False):
 
     `only` (a set of strings, e.g. {"2:512", "5:7"} or, with `widths`, {"8"}) restricts the run to
     the named configurations (N, or N:T for configuration 2's lengths, N:W for configuration 5's
-    widths) or widths, so that a profiler run covers one workload."""
+    widths) or widths, so that a profiler run covers one workload. `x_dtype` is the dtype of x and of
+    the upstream gradient in configuration 2 (bf16 by default, as BASELINE.json states it); the
+    other configurations keep bf16."""
     def want(cfg, sub=None):
         return not only or str(cfg) in only or (sub is not None and f"{cfg}:{sub}" in only)
 
@@ -416,33 +418,35 @@ def run_configs(dev, widths=False, only=None, shapes=False):
             del sets
         return
 
+    dt_tag = "" if x_dtype == torch.bfloat16 else " " + str(x_dtype).replace("torch.", "")
     # Configuration 2: README shape sweep, B=4 D=1024 W=4, weight only or bias + silu.
     for T in (512, 2048, 8192, 32768):
         if not want(2, T):
             continue
         B, D, W = 4, 1024, 4
-        nsets = max(2, min(8, (512 << 20) // (2 * B * T * D * 2)))
-        nfwd = max(2, min(16, (512 << 20) // (B * T * D * 2)))
-        sets = [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16)
+        ex = torch.tensor([], dtype=x_dtype).element_size()
+        nsets = max(2, min(8, (512 << 20) // (2 * B * T * D * ex)))
+        nfwd = max(2, min(16, (512 << 20) // (B * T * D * ex)))
+        sets = [(torch.randn(B, T, D, generator=gen, device=dev).to(x_dtype)
                  .requires_grad_(True),
-                 torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
+                 torch.randn(B, T, D, generator=gen, device=dev).to(x_dtype))
                 for _ in range(nsets)]
         w = (torch.randn(D, W, generator=gen, device=dev) / 2).requires_grad_(True)
         for variant in ("weight_only", "bias_silu"):
             bias = variant == "bias_silu"
             b = torch.randn(D, generator=gen, device=dev).requires_grad_(True) if bias else None
             act = "silu" if bias else None
-            fb, bb = _alg_bytes_general(B, T, D, W, bias)
-            shape = f"B={B} T={T} D={D} W={W} {variant}"
+            fb, bb = _alg_bytes_general(B, T, D, W, bias, ex=ex)
+            shape = f"B={B} T={T} D={D} W={W} {variant}{dt_tag}"
             # forward alone over at least 512 MiB of x, twice the Infinity Cache
-            fsets = sets + [(torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16),
+            fsets = sets + [(torch.randn(B, T, D, generator=gen, device=dev).to(x_dtype),
                              None) for _ in range(max(0, nfwd - nsets))]
             emit("2", shape, timed(fwds(fsets, w, b, act)), fb, bb, "fwd")
             if bias:
                 # The copy ceiling of the forward alone: torch's clone of the same x under the same
                 # rotation (reads and writes the forward's activation bytes, nothing else).
-                emit("2", f"B={B} T={T} D={D} torch clone of x", timed(fwds(fsets, w, b, act,
-                     op=torch.clone)), 2 * B * T * D * 2, 0, "fwd", {"reference": "copy"})
+                emit("2", f"B={B} T={T} D={D}{dt_tag} torch clone of x", timed(fwds(fsets, w, b, act,
+                     op=torch.clone)), 2 * B * T * D * ex, 0, "fwd", {"reference": "copy"})
             del fsets
             emit("2", shape, timed(steps(sets, w, b, act)), fb, bb, "fwd+bwd")
         del sets
@@ -594,6 +598,8 @@ def main():
     ap.add_argument("--only", default="",
                     help="with --configs, --widths or --shapes: comma-separated workloads to run "
                          "(e.g. 2:512,5:7 or, with --widths or --shapes, widths such as 8)")
+    ap.add_argument("--x-dtype", choices=("bf16", "fp16", "fp32"), default="bf16",
+                    help="with --configs: dtype of x and the upstream gradient in configuration 2")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain copies of known size (for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -610,6 +616,8 @@ def main():
     torch.cuda.set_device(dev)
     if args.configs or args.widths or args.shapes:
         run_configs(dev, widths=args.widths, shapes=args.shapes,
+                    x_dtype={"bf16": torch.bfloat16, "fp16": torch.float16,
+                             "fp32": torch.float32}[args.x_dtype],
                     only={t for t in args.only.split(",") if t} or None)
         return
     B, T, D, W = 4, 8192, 1024, 4
