@@ -438,7 +438,18 @@ __global__ __launch_bounds__(NWR * 64) void reduce_partials_kernel(const ReduceP
 #pragma unroll
       for (int u = 0; u < 8; ++u) acc += v[u];
     }
-    for (; q < p.Pn; q += NWR) acc += src[(int64_t)q * rs];
+    // The wave's last 0-7 rows, also all requested before the first add (a loop of load-then-add
+    // waited one memory round trip per row: 2 of them at B=4 T=512 D=1024, 32 partial rows). The
+    // adds keep the row order and skip the rows past Pn.
+    if (q < p.Pn) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (q + u * NWR < p.Pn) v[u] = src[(int64_t)(q + u * NWR) * rs];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (q + u * NWR < p.Pn) acc += v[u];
+    }
   }
   red[wave][lane] = acc;
   __syncthreads();
