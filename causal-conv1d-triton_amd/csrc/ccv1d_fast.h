@@ -758,6 +758,25 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
       }
     };
     int t = t_main;
+    // Passes of U double batches. With 2RU > P rows per pass, every window value live at the
+    // loop's back edge was produced in the pass, so the windows need no register moves there (the
+    // 8-row pass at width 16 moved 30 registers per pass; 16-row passes: B=4 T=8192 D=1024 step
+    // W=9 71.4 -> 70.6 us, W=12 80.3 -> 79.4, W=16 92.9 -> 91.9). Kernels of 2-row batches keep
+    // U = 1: the seq_idx ones were slower with it (configuration 5 at W=7 511 -> 523 us) and the
+    // 4-channel one at width 5 spilled.
+    constexpr int U = (!SEQ && R == 4 && P >= 2 * R && P < 4 * R) ? 2 : 1;
+    if constexpr (U > 1) {
+      for (; t + 2 * R * U <= t_end; t += 2 * R * U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int tu = t + 2 * R * u;
+          load(Bx, By, tu + R);
+          compute(Ax, Ay, tu);
+          load(Ax, Ay, tu + 2 * R);
+          compute(Bx, By, tu + R);
+        }
+      }
+    }
     for (; t + 2 * R <= t_end; t += 2 * R) {
       load(Bx, By, t + R);
       compute(Ax, Ay, t);
