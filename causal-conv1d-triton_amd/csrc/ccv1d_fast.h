@@ -246,6 +246,16 @@ struct FwdLaneRev {
 // together; then a ping-pong over two register batches keeps batch k + 1 in flight while batch k is
 // computed. Rows past the tile end are clamped to its last row: a duplicate read keeps the number of
 // loads in flight independent of the tile length, so the compiler's wait counts stay exact.
+// Double batches (2R rows) per pass of a pipelined row loop: the fewest that make a pass longer
+// than the window of P rows, so each window value live at the loop's back edge was produced in the
+// pass and no register moves are needed there. Kernels of 2-row batches keep one (the seq_idx
+// kernels were slower with more: configuration 5 at W=7 511 -> 523 us; the 4-channel backward at
+// width 5 spilled).
+template <bool SEQ, int R, int P>
+constexpr int pass_batches() {
+  return (!SEQ && R == 4) ? P / (2 * R) + 1 : 1;
+}
+
 template <typename TX, int W, bool SILU, bool SEQ, int CPL, int R, int XLD, int OST, bool DRAIN>
 __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBuf<TX, CPL, XLD>& X,
                                                  const RowBuf<TX, CPL, kCachePlain, OST>& O,
@@ -300,6 +310,22 @@ __device__ __forceinline__ void fwd_tile_forward(const FwdParams& p, const RowBu
   // back edge, and without this wait it waits there for everything, the previous iteration's
   // stores included, every 2R rows; after it, the head waits only for the batch it needs.
   if (DRAIN) __builtin_amdgcn_s_waitcnt(0);
+  // Passes of U double batches, so the window needs no register moves at the loop's back edge
+  // (pass_batches; forward alone at B=4 T=8192 D=1024: W=12 30.2 -> 29.9 us, W=16 32.8 -> 32.2,
+  // W=24 39.1 -> 37.9, W=32 45.7 -> 44.2).
+  constexpr int U = pass_batches<SEQ, R, P>();
+  if constexpr (U > 1) {
+    for (; t + 2 * R * U <= t1; t += 2 * R * U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int tu = t + 2 * R * u;
+        load(B, sB, tu + R);
+        compute(A, sA, tu);
+        load(A, sA, tu + 2 * R);
+        compute(B, sB, tu + R);
+      }
+    }
+  }
   for (; t + 2 * R <= t1; t += 2 * R) {
     load(B, sB, t + R);
     compute(A, sA, t);
@@ -363,6 +389,19 @@ __device__ __forceinline__ void fwd_tile_reverse(const FwdParams& p, const RowBu
   };
   int t = t1 - 1;  // next output row
   if (DRAIN) __builtin_amdgcn_s_waitcnt(0);  // as in fwd_tile_forward
+  constexpr int U = pass_batches<SEQ, R, P>();  // as in fwd_tile_forward
+  if constexpr (U > 1) {
+    for (; t - 2 * R * U + 1 >= t0; t -= 2 * R * U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int tu = t - 2 * R * u;
+        load(B, sB, tu - R - P - 1);
+        compute(A, sA, tu);
+        load(A, sA, tu - 2 * R - P - 1);
+        compute(B, sB, tu - R);
+      }
+    }
+  }
   for (; t - 2 * R + 1 >= t0; t -= 2 * R) {
     load(B, sB, t - R - P - 1);
     compute(A, sA, t);
@@ -758,13 +797,13 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
       }
     };
     int t = t_main;
-    // Passes of U double batches. With 2RU > P rows per pass, every window value live at the
-    // loop's back edge was produced in the pass, so the windows need no register moves there (the
-    // 8-row pass at width 16 moved 30 registers per pass; 16-row passes: B=4 T=8192 D=1024 step
-    // W=9 71.4 -> 70.6 us, W=12 80.3 -> 79.4, W=16 92.9 -> 91.9). Kernels of 2-row batches keep
-    // U = 1: the seq_idx ones were slower with it (configuration 5 at W=7 511 -> 523 us) and the
-    // 4-channel one at width 5 spilled.
-    constexpr int U = (!SEQ && R == 4 && P >= 2 * R && P < 4 * R) ? 2 : 1;
+    // Passes of U double batches (pass_batches). With 2RU > P rows per pass, every window value
+    // live at the loop's back edge was produced in the pass, so the windows need no register moves
+    // there (the 8-row pass at width 16 moved 30 registers per pass; 16-row passes: B=4 T=8192
+    // D=1024 step W=9 71.4 -> 70.6 us, W=12 80.3 -> 79.4, W=16 92.9 -> 91.9; 24-row passes with
+    // the forward's: W=24 128.5 -> 126.1). From width 25 the backward keeps 8-row passes (32-row
+    // passes lost at W=32 what the forward's gained).
+    constexpr int U = P < 6 * R ? pass_batches<SEQ, R, P>() : 1;
     if constexpr (U > 1) {
       for (; t + 2 * R * U <= t_end; t += 2 * R * U) {
 #pragma unroll
