@@ -907,6 +907,25 @@ def test_channels_per_lane_choices(B, T, D, W, xdt):
     compare(gpu, ref, True, cols=cols)
 
 
+@pytest.mark.parametrize("W,xdt", [(9, torch.bfloat16), (12, torch.bfloat16), (16, torch.bfloat16),
+                                   (16, torch.float16), (17, torch.bfloat16), (20, torch.bfloat16),
+                                   (24, torch.float16), (25, torch.bfloat16), (32, torch.bfloat16)])
+def test_row_passes_longer_than_the_window(W, xdt):
+    """From width 9 the pipelined row loops run passes of 2-4 double batches (16-32 rows, longer
+    than the window) before the 8-row passes and the single rows of a tile's end. At B=4 T=8189
+    D=1024 the grid reaches the tilings' wave target with their longest tiles (64 rows in the
+    2-channel forward, 128 in the one-channel passes), so every pass kind runs, and the ragged
+    last tile ends in a different place; against the oracle on a channel subset, without the
+    activation bit-identical."""
+    B, T, D = 4, 8189, 1024
+    cols = _cols(D, 24, 31 * W)
+    for act in ("silu", None):
+        inp = make_inputs(17 * W + (act is None), B, T, D, W, xdt=xdt, init=True)
+        gpu = run_gpu(inp, act, return_final=True, dfinal=True, init_grad=True)
+        ref = oracle_ref(inp, act is not None, cols=cols, final=True, dfinal=True, need_dinit=True)
+        compare(gpu, ref, act is not None, cols=cols)
+
+
 def test_config3_mamba2_xbc():
     """B=8, T=4096, D=5376, W=4; x a channel slice of an in_proj output (time stride 10576)."""
     B, T, D, W = 8, 4096, 5376, 4
