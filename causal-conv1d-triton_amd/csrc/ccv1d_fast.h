@@ -710,6 +710,17 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
   };
 
   float* halo_out = lds + wave * P * COLS + lane * CPL;
+  // The last NS rows of a wave whose pipelined rows number NS modulo R after its whole batches:
+  // every wave with its successor in the workgroup, since tiles are a power of two >= 2R rows long
+  // and the first P rows are peeled. Where a lane's rows are at most 4 bytes they are loaded with
+  // the tile's first requests, so the tile's end does not wait for a load of its own: B=4 D=1024
+  // fwd+bwd T=512 12.62 -> 12.31 us, T=2048 21.2 -> 20.9, B=4 T=8192 W=6 and 8 -0.3 to -0.5 us.
+  // The 4-channel kernels keep the plain loads (benchmark step +0.12 us with them, 2 VGPRs per
+  // row next to the 128 of 4 waves per SIMD), and so do widths from 9 (widths 10 and 19 went past
+  // 128 VGPRs with them).
+  constexpr int NS =
+      (W <= 8 && CPL * sizeof(TX) <= 4) ? ((2 * R - P % (2 * R)) % (2 * R)) % R : 0;
+  raw Sx[NS > 0 ? NS : 1], Sy[NS > 0 ? NS : 1];
   if (active) {
     // The halo rows, the tile's first P rows, the first pipelined batch and the taps are all
     // requested before anything waits on memory (rows past t_end are clamped to the last row).
@@ -740,6 +751,14 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
       }
     }
     load(Ax, Ay, t_main);
+    if constexpr (NS > 0) {
+#pragma unroll
+      for (int r = 0; r < NS; ++r) {
+        const int row = max(t_end - NS + r, t0);
+        Sx[r] = X.ld(row);
+        Sy[r] = PAD ? raw{} : Y.ld(row);
+      }
+    }
     load_taps<W, CPL>(p.w, p.w_dt, p.bias, p.b_dt, p.has_bias, c0, s.wv, s.bv);
     if (SILU && !PAD) {
       // silu' in the base-2 domain (dsilu_scaled): weights and bias times -log2(e).
@@ -825,6 +844,15 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
     if (t + R <= t_end) {
       compute(Ax, Ay, t);
       t += R;
+    }
+    if (NS > 0 && t_end - t == NS) {
+#pragma unroll
+      for (int r = 0; r < NS; ++r) {
+        float dx[CPL];
+        s.step(t + r, Sx[r], Sy[r], SEQ ? ids.at(t + r) : 0, dx);
+        emit_any(t + r - P, dx);
+      }
+      t = t_end;
     }
     for (; t < t_end; ++t) {
       float dx[CPL];
