@@ -273,7 +273,21 @@ constexpr int64_t kBwdSmallGrid = 256;
 // backward): W=12 83.1 -> 80.7 us, W=16 97.9 -> 93.4, W=20 117.1 -> 114.1, W=24 149.6 -> 133.3,
 // W=32 190.5 -> 166.5.
 
-Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int nw, bool seq) {
+// Below kBwdWideW, where the backward takes 2 channels per lane because the 4-channel grid is
+// small, 16-bit x also halves 32-row tiles to 16 while the grid has fewer than
+// kBwdNarrowSmallGrid workgroups (fewer than kTargetWaves waves), and no further. Measured
+// (fwd+bwd step, bias + silu, 32 against 16 rows, same box): bf16 W=4 B=4 T=2048 D=1024 20.8 ->
+// 20.45 us (weight only 20.4 -> 19.6), B=1 T=4096 D=2048 21.4 -> 20.8, B=16 T=256 D=2048 21.2 ->
+// 20.5; W=2 and W=3 0.6-0.9 us faster on those shapes, W=5 0.75 faster on two and even on the
+// third; fp16 W=4 B=4 T=2048 D=1024 21.4 -> 21.2 (weight only 20.7 -> 20.0). Not taken: fp32 x
+// (B=4 T=2048 D=1024 weight only 36.4 -> 36.8), halving 16-row tiles to 8 on such grids (0.1-0.3
+// us slower at B=4 T=1024 D=1024 and B=2 T=2048 D=1024), 16-row tiles at W=8 (0.0-0.8 us slower)
+// and, with one channel per lane, at W=16 (0.0-0.3 us slower).
+constexpr int64_t kBwdNarrowSmallGrid = 512;
+constexpr int kBwdNarrowShortRows = 16;
+
+Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt, int cpl, int nw,
+                      bool seq) {
   const int lmin = min_tile_rows(W);
   const int over = tune().bwd_rows >= lmin ? tune().bwd_rows : 0;
   const int64_t min_time_wg = cpl >= 4 ? kMinTimeWorkgroups : 1;
@@ -281,6 +295,10 @@ Tiling bwd_tiling_for(int64_t B, int64_t T, int64_t D, int64_t W, int cpl, int n
   Tiling t = fast_tiling(B, T, D, cpl, nw, 32, lmax, kTargetWaves, over, min_time_wg);
   while (over == 0 && t.nBlk < kBwdSmallGrid && t.L > lmin)
     t = fast_tiling(B, T, D, cpl, nw, t.L / 2, t.L / 2, kTargetWaves, t.L / 2);
+  if (over == 0 && esize(x_dt) == 2 && W < kBwdWideW && cpl < 4 &&
+      t.L == 2 * kBwdNarrowShortRows && t.nBlk < kBwdNarrowSmallGrid && kBwdNarrowShortRows >= lmin)
+    t = fast_tiling(B, T, D, cpl, nw, kBwdNarrowShortRows, kBwdNarrowShortRows, kTargetWaves,
+                    kBwdNarrowShortRows);
   return t;
 }
 
@@ -313,7 +331,7 @@ FastShape bwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
   } else if (W >= kBwdWideW) {
     sh.cpl = cpl_wide(x_dt);
   } else if (x_dt != CCV1D_F64 && B > 0 && T > 0 && D > 0) {
-    const Tiling t = bwd_tiling_for(B, T, D, W, sh.cpl, sh.nw, false);
+    const Tiling t = bwd_tiling_for(B, T, D, W, x_dt, sh.cpl, sh.nw, false);
     if (D % sh.cpl || t.L < kBwdNarrowMinRows || B * t.nT * t.nGW < kTargetWaves)
       sh.cpl = cpl_wide(x_dt);
   }
@@ -322,7 +340,7 @@ FastShape bwd_shape(int x_dt, int64_t B, int64_t T, int64_t D, int64_t W) {
 
 Tiling bwd_fast_tiling(int64_t B, int64_t T, int64_t D, int64_t W, int x_dt, bool seq) {
   const FastShape sh = bwd_shape(x_dt, B, T, D, W);
-  return bwd_tiling_for(B, T, D, W, sh.cpl, sh.nw, seq);
+  return bwd_tiling_for(B, T, D, W, x_dt, sh.cpl, sh.nw, seq);
 }
 
 // Workspace of the backward: the fp32 partial rows of dweight/dbias, (rows, W + 1, D) floats, and

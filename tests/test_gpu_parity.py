@@ -926,6 +926,27 @@ def test_row_passes_longer_than_the_window(W, xdt):
         compare(gpu, ref, act is not None, cols=cols)
 
 
+@pytest.mark.parametrize("B,T,D,W,xdt,seq", [
+    (4, 2048, 1024, 4, torch.bfloat16, False),
+    (4, 2048, 1024, 2, torch.float16, False),
+    (1, 4096, 2048, 3, torch.bfloat16, False),
+    (16, 256, 2048, 5, torch.float16, False),
+    (4, 2047, 1024, 4, torch.bfloat16, True),    # seq_idx, ragged last tile
+    (4, 2048, 1024, 4, torch.float32, False),    # fp32 keeps 32-row tiles
+])
+def test_small_grid_backward_short_tiles(B, T, D, W, xdt, seq):
+    """Grids whose 2-channel backward falls short of the wave target with 32-row tiles take 16-row
+    tiles for 16-bit x at widths 2-5 (twice the partial dweight rows per column); against the
+    oracle on a channel subset, with initial and final states and their gradients, and with
+    seq_idx."""
+    s = varlen_seq(60 + W, B, T, lo=40, hi=700, pad_frac=0.04) if seq else None
+    inp = make_inputs(B + T + W, B, T, D, W, xdt=xdt, init=True, seq=s)
+    gpu = run_gpu(inp, "silu", return_final=not seq, dfinal=not seq, init_grad=True)
+    cols = _cols(D, 32, T + W)
+    ref = oracle_ref(inp, True, cols=cols, final=not seq, dfinal=not seq, need_dinit=True)
+    compare(gpu, ref, True, cols=cols)
+
+
 def test_config3_mamba2_xbc():
     """B=8, T=4096, D=5376, W=4; x a channel slice of an in_proj output (time stride 10576)."""
     B, T, D, W = 8, 4096, 5376, 4
