@@ -629,11 +629,12 @@ constexpr int bwd_waves_per_simd() {
 }
 
 // LDS of the backward: first the g values of every wave's first P rows (the right halo of the wave
-// before it), later the dweight/dbias sums of waves 1..NW-1.
+// before it), later the dweight/dbias sums of every wave (at most 8 x 33 x 64 floats, 66 KiB, at
+// width 32, whose kernels run one workgroup per CU; 40 KiB at width 4 with 4 channels per lane).
 template <int W, int CPL, int NW>
 constexpr int bwd_lds_floats() {
   constexpr int halo = NW * (W - 1) * 64 * CPL;
-  constexpr int red = (NW > 1 ? NW - 1 : 1) * (W + 1) * 64 * CPL;
+  constexpr int red = NW * (W + 1) * 64 * CPL;
   return halo > red ? halo : red;
 }
 
@@ -904,32 +905,49 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
     }
   }
 
-  // Workgroup sum of dweight/dbias in wave order 0, 1, ..., NW-1, then one partial row. The halo
-  // area of LDS is reused, after every wave has read its neighbour's halo.
-  if (NW > 1) {
+  // Workgroup sum of dweight/dbias, then one partial row of W + 1 rows (dbias last). Every wave puts
+  // its sums in LDS (the halo area is reused, after every wave has read its neighbour's halo), and
+  // wave v sums rows v, v + NW, ... over the NW waves in wave order 0, 1, ..., NW-1 and stores
+  // them. A row's reads are requested 4 waves at a time, so the workgroup's end waits two LDS round
+  // trips where wave 0 alone, adding one wave's rows at a time, waited NW - 1 (all NW at once took
+  // some instances past their register budget: width 5 with 4 channels per lane spilled, widths 19
+  // and 20 went past 128 VGPRs).
+  const int n_rows = p.has_bias ? W + 1 : W;
+  if constexpr (NW > 1) {
     lds_barrier();
-    if (wave > 0) {
-      float* dst = lds + (wave - 1) * (W + 1) * COLS + lane * CPL;
+    float* dst = lds + wave * (W + 1) * COLS + lane * CPL;
 #pragma unroll
-      for (int k = 0; k < W; ++k)
+    for (int k = 0; k < W; ++k)
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) dst[k * COLS + i] = s.dw[k][i];
+      for (int i = 0; i < CPL; ++i) dst[k * COLS + i] = s.dw[k][i];
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) dst[W * COLS + i] = s.db[i];
-    }
+    for (int i = 0; i < CPL; ++i) dst[W * COLS + i] = s.db[i];
     lds_barrier();
-  }
-  if (wave == 0 && grp < G) {
+    if (grp < G) {
+      float* pp = p.part + ((int64_t)tc.b * p.tl.nTB + tc.tb) * (W + 1) * D + c0;
 #pragma unroll 1
-    for (int v = 1; v < NW; ++v) {
-      const float* src = lds + (v - 1) * (W + 1) * COLS + lane * CPL;
+      for (int k = wave; k < n_rows; k += NW) {
+        constexpr int VG = NW < 4 ? NW : 4;  // waves' rows read together
+        static_assert(NW % VG == 0, "the groups of reads cover the workgroup's waves");
+        float acc[CPL];
 #pragma unroll
-      for (int k = 0; k < W; ++k)
+        for (int v0 = 0; v0 < NW; v0 += VG) {
+          float c[VG][CPL];
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) s.dw[k][i] += src[k * COLS + i];
+          for (int v = 0; v < VG; ++v)
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) s.db[i] += src[W * COLS + i];
+            for (int i = 0; i < CPL; ++i)
+              c[v][i] = lds[((v0 + v) * (W + 1) + k) * COLS + lane * CPL + i];
+#pragma unroll
+          for (int v = 0; v < VG; ++v)
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) acc[i] = (v0 + v == 0) ? c[v][i] : acc[i] + c[v][i];
+        }
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) pp[k * D + i] = acc[i];
+      }
     }
+  } else if (grp < G) {
     float* pp = p.part + ((int64_t)tc.b * p.tl.nTB + tc.tb) * (W + 1) * D + c0;
 #pragma unroll
     for (int k = 0; k < W; ++k)
