@@ -864,17 +864,50 @@ __device__ __forceinline__ void bwd_tile(const BwdParams& p, float* lds, const R
     if (succ_here) {
       // The last P dx rows, from the next wave's g of rows own_end .. own_end + P - 1.
       const float* halo_in = lds + (wave + 1) * P * COLS + lane * CPL;
+      if constexpr (W <= 8) {
+        // All P rows are read from LDS before the first is used (read one by one, between the
+        // stores of the rows before, each waited a round trip of its own), and their dx rows,
+        // own_end - P .. own_end - 1, all lie in x (the tile is longer than P), so they skip the
+        // initial-state branches. From width 9 the rows stay read one by one: the P x CPL registers
+        // (and the changed schedule) took widths 19 and 20 past 128 VGPRs.
+        float gh[P][CPL];
 #pragma unroll
-      for (int q = 0; q < P; ++q) {
-        const int tt = own_end + q;
-        float g[CPL], dx[CPL];
+        for (int q = 0; q < P; ++q)
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) g[i] = halo_in[q * COLS + i];
-        const int32_t st = SEQ ? ids.at(tt) : 0;
-        s.dx_row(g, st, true, dx);
-        emit_any(tt - P, dx);
-        shift_in(s.gw, g);
-        if (SEQ) shift_in(s.sw, st);
+          for (int i = 0; i < CPL; ++i) gh[q][i] = halo_in[q * COLS + i];
+#pragma unroll
+        for (int q = 0; q < P; ++q) {
+          const int tt = own_end + q;
+          float dx[CPL];
+          const int32_t st = SEQ ? ids.at(tt) : 0;
+          s.dx_row(gh[q], st, true, dx);
+          const int row = tt - P;
+          if (dfb) {
+            const int f = row - (T - P);
+            if (f >= 0) {
+              float d[CPL];
+              IO::unpack(IO::ld(dfb + f * D), d);
+#pragma unroll
+              for (int i = 0; i < CPL; ++i) dx[i] += d[i];
+            }
+          }
+          DX.st(row, IO::pack(dx));
+          shift_in(s.gw, gh[q]);
+          if (SEQ) shift_in(s.sw, st);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < P; ++q) {
+          const int tt = own_end + q;
+          float g[CPL], dx[CPL];
+#pragma unroll
+          for (int i = 0; i < CPL; ++i) g[i] = halo_in[q * COLS + i];
+          const int32_t st = SEQ ? ids.at(tt) : 0;
+          s.dx_row(g, st, true, dx);
+          emit_any(tt - P, dx);
+          shift_in(s.gw, g);
+          if (SEQ) shift_in(s.sw, st);
+        }
       }
     } else if (t_end == T) {
       // Rows past the end of the sequence have g = 0 and sequence id -1.
