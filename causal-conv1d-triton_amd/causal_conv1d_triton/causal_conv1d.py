@@ -42,7 +42,9 @@ def _check_inputs(x, weight, bias, seq_idx, initial_states):
     if seq_idx is not None:
         assert seq_idx.shape == (B, T), "seq_idx must be (batch, seqlen)"
         assert seq_idx.get_device() == dev, "seq_idx must be on the device of x"
-    # Offsets within one batch element are computed in int32.
+    # The library indexes the elements of one batch row, halo included, with 32-bit signed offsets
+    # (the C ABI refuses larger rows; its vectorised kernels also need the byte offsets below 2^32
+    # and otherwise take the generic ones).
     st = x.stride(1)
     assert (T + W) * (st if st > D else D) < 2**31, "seqlen * dim too large for 32-bit offsets"
 
