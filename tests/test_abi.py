@@ -104,6 +104,26 @@ def test_workspace_bytes_for_the_call():
         assert 0 < n <= lib.ccv1d_bwd_workspace_bytes(B, T, D, W, xdt), (B, T, D, W, xdt)
 
 
+def test_small_grid_backward_tiles():
+    """The vectorised backward writes one partial row ((W + 1) x dim fp32) per batch row and
+    workgroup of 8 tiles along time, so its workspace shows the tiling. At B=4 D=1024 the 4-channel
+    grid is small and the backward takes 2 channels per lane: at T=2048 W=4 its 32-row tiles leave
+    256 workgroups, and 16-bit x halves them to 16 rows (16 workgroups along time per batch row)
+    while fp32 x keeps 32 (8), as does 16-bit x from width 6; at T=512 the tiles shrink to 8 rows
+    for fewer than 256 workgroups, whatever the dtype."""
+    lib = _ffi.load()
+    row = 5 * 1024 * 4
+    assert _ws_for(lib, T=2048, xdt=2) == 4 * 16 * row   # bf16
+    assert _ws_for(lib, T=2048, xdt=1) == 4 * 16 * row   # fp16
+    assert _ws_for(lib, T=2048, xdt=0) == 4 * 8 * row    # fp32
+    assert _ws_for(lib, T=2048, W=8) == 4 * 8 * 9 * 1024 * 4
+    assert _ws_for(lib, T=512, xdt=2) == 4 * 8 * row
+    assert _ws_for(lib, T=512, xdt=0) == 4 * 8 * row
+    # never above the shape-only bound the default backward allocates
+    for xdt in (0, 1, 2):
+        assert _ws_for(lib, T=2048, xdt=xdt) <= lib.ccv1d_bwd_workspace_bytes(4, 2048, 1024, 4, xdt)
+
+
 def _fwd(lib, **kw):
     a = dict(x=1 << 20, sxb=0, sxt=8, xdt=2, w=1 << 21, wdt=0, b=None, bdt=0, seq=None, init=None,
              idt=0, out=1 << 22, fin=None, B=1, T=4, D=8, W=4, silu=1, dev=0, stream=None)
